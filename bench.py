@@ -1,0 +1,308 @@
+"""Benchmark of the matmul hot path on one MI355X (BASELINE.json metric, config C2).
+
+A step is one decode token of Llama-3.1-8B at batch 1 through every matmul of the model: per
+layer the fused RMSNorm + QKV + RoPE + KV-write GEMV, o_proj + residual, fused RMSNorm + gate/up +
+SwiGLU, down + residual (the reference's decode_step order, api.cu:1891-1952, attention aside),
+then the RMSNorm + lm_head GEMV. All 32 layers' distinct weight sets (15.0 GB fp16, 7.5 GB int8 +
+row scales) are streamed once per token from HBM, so the 256 MB MALL cannot serve them. The token
+is captured once as a hipGraph and replayed. Weights ~N(0, 0.02), activations and norm weights
+seeded; everything is generated on the GPU (synthetic data, random-init weights of the
+architecture).
+
+value: fp16 decode-GEMV throughput in GB/s = algorithmic weight bytes per token / time per token.
+Also reported: the int8 token, each GEMV kind alone, the prefill GEMM (C3) when built, the
+dominant kernel's roofline (gate/up GEMV, timed with HIP events on the stream it runs on), and the
+CPU baseline (the oracle's GEMV restatement on one layer, timed on the host cores).
+
+python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, datasheet
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, datasheet
+
+# Llama-3.1-8B
+H, HQ, HKV, D, I, V, L = 4096, 32, 8, 128, 14336, 128256, 32
+QKV = (HQ + 2 * HKV) * D
+SHAPES = {"qkv": (QKV, H), "o": (H, HQ * D), "gate_up": (2 * I, H), "down": (H, I)}
+SEED = 1219 + 1
+
+
+def weight_bytes(q8):
+    """Algorithmic bytes per token the reference counts (bench.py:147,234): N*K*w + 2N scales."""
+    w = 1 if q8 else 2
+    per_layer = sum(N * K * w + (2 * N if q8 else 0) for N, K in SHAPES.values())
+    return per_layer * L + V * H * w + (2 * V if q8 else 0)
+
+
+def act_bytes():
+    """Activation/output bytes per token on top of the weights (x reads, out writes, residual reads,
+    the K/V cache writes), each counted once per GEMV."""
+    per_layer = (H * 2 + QKV * 2) + (HQ * D * 2 + 2 * H * 2) + (H * 2 + I * 2) + (I * 2 + 2 * H * 2)
+    return per_layer * L + H * 2 + V * 2
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Model:
+    def __init__(self, torch, hi, q8_too=True):
+        self.torch, self.hi = torch, hi
+        dev = "cuda"
+        g = torch.Generator(device=dev)
+        g.manual_seed(SEED)
+
+        def w(N, K):
+            return torch.empty(N, K, dtype=torch.float16, device=dev).normal_(0.0, 0.02, generator=g)
+
+        def nrm(n):
+            return (torch.rand(n, generator=g, device=dev) + 0.5).half()
+
+        self.layers = []
+        for _ in range(L):
+            ly = {k: w(*s) for k, s in SHAPES.items()}
+            ly["n1"], ly["n2"] = nrm(H), nrm(H)
+            self.layers.append(ly)
+        self.lm = w(V, H)
+        self.nf = nrm(H)
+        self.q8 = None
+        if q8_too:
+            self.q8 = []
+            for ly in self.layers:
+                self.q8.append({k: hi.quantize_rows(ly[k]) for k in SHAPES})
+            self.lm_q = hi.quantize_rows(self.lm)
+        self.max_seq = 64
+        self.kc = [torch.zeros(1, HKV, self.max_seq, D, dtype=torch.float16, device=dev) for _ in range(L)]
+        self.vc = [torch.zeros_like(k) for k in self.kc]
+        ang = torch.arange(self.max_seq, device=dev).float()[:, None] * (
+            1.0 / 500000.0 ** (torch.arange(0, D, 2, device=dev).float() / D))[None, :]
+        self.cs = torch.stack([ang.cos(), ang.sin()], -1).half().contiguous()
+        self.pos = torch.tensor([7], dtype=torch.int32, device=dev)
+        self.x = torch.randn(1, H, generator=g, device=dev).half()
+        self.x0 = self.x.clone()
+        self.q = torch.empty(1, HQ * D, dtype=torch.float16, device=dev)
+        self.act = torch.empty(1, I, dtype=torch.float16, device=dev)
+        self.logits = torch.empty(1, V, dtype=torch.float16, device=dev)
+        torch.cuda.synchronize()
+
+    def _w(self, l, name, q8):
+        if not q8:
+            return self.layers[l][name], None
+        return self.q8[l][name]
+
+    def token(self, q8):
+        """One decode token through every matmul of the model (fused epilogues as the engine runs them)."""
+        hi = self.hi
+        self.x.copy_(self.x0)
+        for l in range(L):
+            W, s = self._w(l, "qkv", q8)
+            hi.gemv_qkv_rope(self.x, W, self.layers[l]["n1"], HQ, HKV, self.cs, self.pos, self.kc[l], self.vc[l], self.q,
+                             scales=s)
+            W, s = self._w(l, "o", q8)
+            hi.gemv(self.q, W, out=self.x, epi=1, scales=s)
+            W, s = self._w(l, "gate_up", q8)
+            hi.gemv(self.x, W, out=self.act, normw=self.layers[l]["n2"], epi=2, scales=s)
+            W, s = self._w(l, "down", q8)
+            hi.gemv(self.act, W, out=self.x, epi=1, scales=s)
+        W, s = (self.lm, None) if not q8 else self.lm_q
+        hi.gemv(self.x, W, out=self.logits, normw=self.nf, scales=s)
+
+    def one_kind(self, kind, q8):
+        """The 32 layers' GEMVs of one kind back to back (or the lm_head 4 times)."""
+        hi = self.hi
+        if kind == "lm_head":
+            W, s = (self.lm, None) if not q8 else self.lm_q
+            for _ in range(4):
+                hi.gemv(self.x, W, out=self.logits, normw=self.nf, scales=s)
+            return 4
+        for l in range(L):
+            W, s = self._w(l, kind, q8)
+            if kind == "qkv":
+                hi.gemv_qkv_rope(self.x, W, self.layers[l]["n1"], HQ, HKV, self.cs, self.pos, self.kc[l], self.vc[l],
+                                 self.q, scales=s)
+            elif kind == "o":
+                hi.gemv(self.q, W, out=self.x, epi=1, scales=s)
+            elif kind == "gate_up":
+                hi.gemv(self.x, W, out=self.act, normw=self.layers[l]["n2"], epi=2, scales=s)
+            else:
+                hi.gemv(self.act, W, out=self.x, epi=1, scales=s)
+        return L
+
+
+def capture(torch, fn):
+    fn()  # eager warm-up: per-kernel attributes and occupancy are set outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, steps, warmup):
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    return e0.elapsed_time(e1) / steps, wall / steps
+
+
+def cpu_baseline(torch, model, budget_s=12.0):
+    """The oracle's restatement of the reference's CPU path (fp16(fp32-or-better x @ W^T) with the
+    same epilogues) on one Llama-3.1-8B layer's four GEMVs (fp16 weights copied from the GPU),
+    repeated for about budget_s seconds on the host's cores. Returns GB/s of weight bytes."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import oracle as O
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", "16"))))
+    O.set_threads(cores)
+    ly = model.layers[0]
+    Wh = {k: ly[k].cpu().numpy() for k in SHAPES}
+    n1, n2 = ly["n1"].cpu().numpy(), ly["n2"].cpu().numpy()
+    cs, pos = model.cs.cpu().numpy(), np.array([7], np.int32)
+    rng = np.random.default_rng(SEED)
+    x = rng.standard_normal((1, H)).astype(np.float16)
+    kc = np.zeros((1, HKV, model.max_seq, D), np.float16)
+    vc = np.zeros_like(kc)
+    q = np.zeros((1, HQ * D), np.float16)
+    act = np.zeros((1, I), np.float16)
+    nbytes = sum(N * K * 2 for N, K in SHAPES.values())
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        xs = x.copy()
+        t0 = time.perf_counter()
+        O.gemv_qkv_rope(xs, Wh["qkv"], n1, HQ, HKV, cs, pos, kc, vc, q)
+        O.gemv(q, Wh["o"], out=xs, epi=1)
+        O.gemv(xs, Wh["gate_up"], out=act, normw=n2, epi=2)
+        O.gemv(act, Wh["down"], out=xs, epi=1)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": O.get_threads(), "kind": "port",
+            "sample": f"one Llama-3.1-8B layer's 4 decode GEMVs (QKV+RoPE, o+res, gate/up+SwiGLU, down+res; "
+                      f"{nbytes / 1e6:.1f} MB fp16 weights, M=1), oracle/hi_oracle.c with OpenMP, median of "
+                      f"{len(times)} repetitions ({sum(times):.1f} s)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-int8", action="store_true")
+    ap.add_argument("--profile", choices=["gate_up", "token"], default=None,
+                    help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (the matmul hot path on one MI355X); "
+              f"--gpus {args.gpus} / WORLD_SIZE {world} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from hipinfer_amd import hipinfer as hi
+
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    log(f"device: {torch.cuda.get_device_name(0)}, {hi.lib.hi_device_cus()} CUs")
+    t0 = time.perf_counter()
+    model = Model(torch, hi, q8_too=not args.no_int8)
+    log(f"weights ready in {time.perf_counter() - t0:.1f} s")
+
+    if args.profile:
+        fn = (lambda: model.one_kind("gate_up", False)) if args.profile == "gate_up" else (lambda: model.token(False))
+        g = capture(torch, fn)
+        for _ in range(args.steps):
+            g.replay()
+        torch.cuda.synchronize()
+        # a plain device copy of known size, to calibrate the HBM byte counters
+        src = torch.empty(1 << 29, dtype=torch.float16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"profile run done ({args.profile}); copy kernel moved {src.numel() * 2} bytes each way x3")
+        return
+
+    # ---- the step: one fp16 token through all 32 layers + lm_head
+    g16 = capture(torch, lambda: model.token(False))
+    ms16, wall16 = time_graph(torch, g16, args.steps, args.warmup)
+    assert torch.isfinite(model.logits).all(), "non-finite logits"
+    out = {"fp16": (ms16, wall16)}
+    kernels = {}
+    if model.q8 is not None:
+        g8 = capture(torch, lambda: model.token(True))
+        ms8, wall8 = time_graph(torch, g8, args.steps, args.warmup)
+        assert torch.isfinite(model.logits).all(), "non-finite logits (int8)"
+        out["int8"] = (ms8, wall8)
+    # ---- each GEMV kind alone (32 distinct weight sets back to back), fp16 and int8
+    for q8 in ([False, True] if model.q8 is not None else [False]):
+        for kind in ["qkv", "o", "gate_up", "down", "lm_head"]:
+            n = [0]
+
+            def fn(kind=kind, q8=q8):
+                n[0] = model.one_kind(kind, q8)
+            g = capture(torch, fn)
+            ms, _ = time_graph(torch, g, max(3, args.steps // 2), 2)
+            N, K = SHAPES[kind] if kind != "lm_head" else (V, H)
+            b = N * K * (1 if q8 else 2) + (2 * N if q8 else 0)
+            us = ms * 1e3 / n[0]
+            kernels[f"{kind}_{'int8' if q8 else 'fp16'}"] = {
+                "N": N, "K": K, "us": round(us, 2), "GB/s": round(b / us / 1e3, 1),
+                "pct_hbm_peak": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 1)}
+    gu = kernels["gate_up_fp16"]
+    N, K = SHAPES["gate_up"]
+    alg = N * K * 2 + (H * 2 + (N // 2) * 2 + H * 2)  # weights + x + out + norm weight
+    roofline = {"bound": "hbm", "achieved": round(alg / gu["us"] / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(alg / gu["us"] / 1e3 / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "gemv_kernel<MR=1,NORM,EPI=2 (SwiGLU),fp16> gate/up 28672x4096",
+                "launch_bytes": alg, "avg_us": gu["us"]}
+
+    wb16 = weight_bytes(False)
+    value = wb16 / (ms16 * 1e-3) / 1e9
+    res = {
+        "metric": "decode GEMV GB/s (% HBM peak) + prefill GEMM TFLOP/s, 8B shapes fp16/int8",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms16, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic (seeded N(0,0.02) weights of the architecture, generated on the GPU)",
+        "config": {"workload": "Llama-3.1-8B decode GEMV set, batch 1: 32 layers x (QKV+RoPE, o, gate/up, down) + "
+                               "lm_head, every weight streamed once per token (hipGraph replay)",
+                   "weight_bytes_per_step": wb16, "act_bytes_per_step": act_bytes()},
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "wall_ms_per_step": round(wall16, 4),
+    }
+    if "int8" in out:
+        wb8 = weight_bytes(True)
+        v8 = wb8 / (out["int8"][0] * 1e-3) / 1e9
+        res["int8"] = {"value": round(v8, 1), "unit": "GB/s", "ms_per_step": round(out["int8"][0], 4),
+                       "pct_hbm_peak": round(100 * v8 / HBM_PEAK_GBS, 2), "weight_bytes_per_step": wb8}
+    res["kernels"] = kernels
+    res["roofline"] = roofline
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        res["cpu_baseline"] = cpu_baseline(torch, model)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,274 @@
+// Decode GEMV for gfx950: out[m, n] (epi) sum_k x[m, k] * W[n, k] for M <= 16 activation rows.
+//
+// Replaces the reference's gemv_kernel<MR, NORM, EPI, Q8> (src/kernels.cuh:164-281) behind the
+// same C-ABI (hi_gemv, hi_gemv_w8, hi_gemv_qkv_rope, hi_gemv_qkv_rope_w8; api.cu:181-230).
+//
+// Design (weight-bandwidth bound; the activation rows are tiny and live in LDS):
+//  * the block stages the M activation rows in LDS once, RMSNorm'd on the way when normw is
+//    given (fused prologue, HF rounding order);
+//  * each wave owns one output unit at a time (one weight row, or the row pair an epilogue
+//    combines) and streams it with 128-bit loads, lane l taking 16-byte chunks l, l+64, ...,
+//    U loads per row in flight;
+//  * int8 chunks are unpacked to exact fp16 in registers (v_perm_b32 + one packed fp16 sub per
+//    two weights) and every pair of weights meets its activation pair in one v_dot2_f32_f16
+//    (fp32 accumulate);
+//  * a fixed DPP/swizzle butterfly reduces each row over the wave; the int8 row scale is applied
+//    once to the reduced sum, then the epilogue runs on lane m for activation row m.
+// A row's arithmetic never depends on M, the unit schedule or the grid: row m of an M-row GEMV is
+// bit-identical to the 1-row GEMV of that row (the reference's promise, api.cu:153-155, that
+// speculative verification relies on).
+#pragma once
+#include "hi_common.h"
+
+// Weight formats: fp16; int8 streamed 16 weights per 16-byte load (K % 16 == 0); int8 streamed
+// 8 weights per 8-byte load (K % 16 == 8, where rows are only 8-byte aligned).
+enum { WF_F16 = 0, WF_I8 = 1, WF_I8H = 2 };
+
+struct GemvArgs {
+  const f16* x;
+  int64_t ldx;
+  const f16* normw;  // fused RMSNorm weight [K] or nullptr
+  float eps;
+  const void* W;     // [N, K] fp16 or int8
+  const f16* scales; // [N] int8 row scales, or nullptr
+  f16* out;
+  int64_t ldo;
+  int M, N, K;
+  // epilogue 3: QKV + bias + RoPE + KV-cache write
+  const f16* bias;   // [(Hq + 2 Hkv) D] or nullptr
+  const f16x2* cs;   // [max_seq][D/2] (cos, sin)
+  const int* pos;    // [M] position of each row (already offset to this launch's first row)
+  f16* kc;
+  f16* vc;           // caches [slots][Hkv][max_seq][D]
+  int max_seq, Hq, Hkv, D, kv_slot, slot_base;
+};
+
+template <int WF> struct WLoad { typedef u32x4 T; };
+template <> struct WLoad<WF_I8H> { typedef u32x2 T; };
+
+template <int MR, bool NORM, int EPI, int WF>
+__global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
+  constexpr int NR = EPI >= 2 ? 2 : 1;                  // weight rows per output unit
+  constexpr int WPL = WF == WF_I8 ? 16 : 8;             // weights per load
+  constexpr int XPL = WPL / 8;                          // 16-byte activation chunks per load
+  constexpr int WB = WF == WF_F16 ? 16 : WPL;           // bytes per load
+  constexpr int U = WF == WF_I8 ? 4 : 8;                // loads per row in flight
+  typedef typename WLoad<WF>::T LT;
+  extern __shared__ u32x4 xs[];                         // [MR][K / 8] activation chunks
+  __shared__ float red[4][MR];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = a.K, K8 = K >> 3, M = a.M;
+
+  // ---- stage the activation rows (rows >= M are zero so no garbage reaches the sums)
+  if constexpr (NORM) {
+    float ss[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) ss[m] = 0.f;
+    for (int i = tid; i < K8; i += 256) {
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        if (m < M) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * i);
+#pragma unroll
+          for (int p = 0; p < 4; p++) {
+            const f16x2 h = as_h2(v[p]);
+            ss[m] = dot2(h, h, ss[m]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; m++) ss[m] = wave_sum(ss[m]);
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MR; m++) red[wave][m] = ss[m];
+    }
+    __syncthreads();
+    float r[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      const float tot = (red[0][m] + red[1][m]) + (red[2][m] + red[3][m]);
+      r[m] = 1.0f / __builtin_sqrtf(tot / (float)K + a.eps);
+    }
+    for (int i = tid; i < K8; i += 256) {
+      const u32x4 wv = *reinterpret_cast<const u32x4*>(a.normw + 8 * i);
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        u32x4 o = {0u, 0u, 0u, 0u};
+        if (m < M) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * i);
+#pragma unroll
+          for (int p = 0; p < 4; p++) {
+            const f16x2 xh = as_h2(v[p]), wh = as_h2(wv[p]);
+            f16x2 y;
+            y.x = wh.x * (f16)((float)xh.x * r[m]);  // w * fp16(x * r), fp16 product (HF order)
+            y.y = wh.y * (f16)((float)xh.y * r[m]);
+            o[p] = as_u32(y);
+          }
+        }
+        xs[m * K8 + i] = o;
+      }
+    }
+  } else {
+    for (int i = tid; i < MR * K8; i += 256) {
+      const int m = i / K8, c = i - m * K8;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (m < M) v = *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c);
+      xs[i] = v;
+    }
+  }
+  __syncthreads();
+
+  const int n_units = EPI >= 2 ? a.N / 2 : a.N;
+  const int nload = K / WPL;
+  const int64_t row_bytes = (int64_t)K * (WF == WF_F16 ? 2 : 1);
+  const char* Wb = reinterpret_cast<const char*>(a.W);
+  const int nw = gridDim.x * 4;
+
+  for (int u = blockIdx.x * 4 + wave; u < n_units; u += nw) {
+    int rows[NR];
+    if constexpr (EPI <= 1) {
+      rows[0] = u;
+    } else if constexpr (EPI == 2) {  // gate/up interleaved in groups of 16 rows
+      rows[0] = (u >> 4) * 32 + (u & 15);
+      rows[NR - 1] = rows[0] + 16;
+    } else {  // rows d and d + D/2 of one head
+      const int HD = a.D >> 1;
+      rows[0] = (u / HD) * a.D + u % HD;
+      rows[NR - 1] = rows[0] + HD;
+    }
+    const char* wr[NR];
+#pragma unroll
+    for (int j = 0; j < NR; j++) wr[j] = Wb + rows[j] * row_bytes;
+
+    float acc[NR][MR];
+#pragma unroll
+    for (int j = 0; j < NR; j++)
+#pragma unroll
+      for (int m = 0; m < MR; m++) acc[j][m] = 0.f;
+
+    for (int base = 0; base < nload; base += 64 * U) {
+      LT wv[NR][U];
+#pragma unroll
+      for (int i = 0; i < U; i++) {
+        const int c = base + i * 64 + lane;
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+          if (c < nload) wv[j][i] = *reinterpret_cast<const LT*>(wr[j] + (int64_t)c * WB);
+          else wv[j][i] = LT{};
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < U; i++) {
+        const int c = base + i * 64 + lane;
+        if (c < nload) {
+          f16x2 wp[NR][WPL / 2];
+#pragma unroll
+          for (int j = 0; j < NR; j++) {
+            if constexpr (WF == WF_F16) {
+#pragma unroll
+              for (int p = 0; p < 4; p++) wp[j][p] = as_h2(wv[j][i][p]);
+            } else {
+#pragma unroll
+              for (int p = 0; p < WPL / 4; p++) i8x4_to_f16(wv[j][i][p], wp[j][2 * p], wp[j][2 * p + 1]);
+            }
+          }
+#pragma unroll
+          for (int m = 0; m < MR; m++) {
+#pragma unroll
+            for (int t = 0; t < XPL; t++) {
+              const u32x4 xv = xs[m * K8 + c * XPL + t];
+#pragma unroll
+              for (int p = 0; p < 4; p++) {
+                const f16x2 xp = as_h2(xv[p]);
+#pragma unroll
+                for (int j = 0; j < NR; j++) acc[j][m] = dot2(wp[j][4 * t + p], xp, acc[j][m]);
+              }
+            }
+          }
+        }
+      }
+    }
+
+#pragma unroll
+    for (int j = 0; j < NR; j++)
+#pragma unroll
+      for (int m = 0; m < MR; m++) acc[j][m] = wave_sum(acc[j][m]);
+
+    if (lane < MR && lane < M) {
+      float a0 = 0.f, a1 = 0.f;  // this lane's row, selected without dynamic register indexing
+#pragma unroll
+      for (int m = 0; m < MR; m++)
+        if (m == lane) {
+          a0 = acc[0][m];
+          a1 = acc[NR - 1][m];
+        }
+      if constexpr (WF != WF_F16) {
+        a0 *= (float)a.scales[rows[0]];
+        a1 *= (float)a.scales[rows[NR - 1]];
+      }
+      f16* orow = a.out + lane * a.ldo;
+      if constexpr (EPI == 0) {
+        orow[u] = (f16)a0;
+      } else if constexpr (EPI == 1) {
+        orow[u] = orow[u] + (f16)a0;  // fp16 add, correctly rounded
+      } else if constexpr (EPI == 2) {
+        orow[u] = silu_mul(a0, a1);
+      } else {
+        const int D = a.D, HD = D >> 1, head = u / HD, d = u - head * HD;
+        const int p = a.pos[lane];
+        const int slot = a.kv_slot >= 0 ? a.kv_slot : a.slot_base + lane;
+        if (a.bias) {
+          a0 += (float)a.bias[rows[0]];
+          a1 += (float)a.bias[rows[NR - 1]];
+        }
+        f16 y1 = (f16)a0, y2 = (f16)a1;
+        if (head < a.Hq + a.Hkv) rope_pair(y1, y2, a.cs[(int64_t)p * HD + d]);
+        f16* dst;
+        if (head < a.Hq) dst = orow + head * D;
+        else if (head < a.Hq + a.Hkv) dst = a.kc + (((int64_t)slot * a.Hkv + head - a.Hq) * a.max_seq + p) * D;
+        else dst = a.vc + (((int64_t)slot * a.Hkv + head - a.Hq - a.Hkv) * a.max_seq + p) * D;
+        dst[d] = y1;
+        dst[d + HD] = y2;
+      }
+    }
+  }
+}
+
+// One launch: the grid fills the resident block slots once, every wave taking the same number
+// of units (within one), so the fused-norm prologue is paid once per block.
+template <int MR, bool NORM, int EPI, int WF>
+int gemv_launch(const GemvArgs& a, hipStream_t s) {
+  const HiDevice* d = hi_device();
+  if (!d) return -2;
+  const size_t lds = (size_t)MR * a.K * 2;
+  const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MR, NORM, EPI, WF>);
+  const int bpc = hi_blocks_per_cu(fn, 256, lds);
+  if (bpc < 0) return -2;
+  if (bpc == 0) HI_FAIL("gemv: %zu bytes of activation rows do not fit in LDS", lds);
+  const int n_units = EPI >= 2 ? a.N / 2 : a.N;
+  const int slots = bpc * d->cus * 4;
+  const int per_wave = (n_units + slots - 1) / slots;
+  const int grid = (n_units + 4 * per_wave - 1) / (4 * per_wave);
+  hipLaunchKernelGGL((gemv_kernel<MR, NORM, EPI, WF>), dim3(grid), dim3(256), lds, s, a);
+  HI_TRY(hipGetLastError());
+  return 0;
+}
+
+// Template selection for one epilogue (each epilogue's instances live in their own file).
+template <int EPI>
+int gemv_run(const GemvArgs& a, int MR, bool norm, int wf, hipStream_t s);
+
+#define HI_GEMV_CASE(mr, nm, wfv) \
+  if (MR == mr && norm == nm && wf == wfv) return gemv_launch<mr, nm, EPI, wfv>(a, s);
+#define HI_GEMV_WF(mr, nm) HI_GEMV_CASE(mr, nm, WF_F16) HI_GEMV_CASE(mr, nm, WF_I8) HI_GEMV_CASE(mr, nm, WF_I8H)
+#define HI_GEMV_DEFINE_RUN(EPIV)                                                                  \
+  template <>                                                                                     \
+  int gemv_run<EPIV>(const GemvArgs& a, int MR, bool norm, int wf, hipStream_t s) {              \
+    constexpr int EPI = EPIV;                                                                     \
+    HI_GEMV_WF(1, true) HI_GEMV_WF(2, true) HI_GEMV_WF(4, true) HI_GEMV_WF(8, true)               \
+    HI_GEMV_WF(1, false) HI_GEMV_WF(2, false) HI_GEMV_WF(4, false) HI_GEMV_WF(8, false)           \
+    HI_GEMV_WF(16, false)                                                                         \
+    HI_FAIL("gemv: no kernel for %d rows (norm %d, format %d)", MR, (int)norm, wf);               \
+  }

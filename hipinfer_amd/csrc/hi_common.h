@@ -1,0 +1,117 @@
+// Shared device/host pieces of the MI355X (gfx950, CDNA4, wave64) matmul hot path.
+// fp16 storage, fp32 accumulation; every fp16 rounding point of the reference kernels
+// (src/kernels.cuh:1-3) is kept at the same place.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+
+#define HI_EXPORT extern "C" __attribute__((visibility("default")))
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------ host-side error reporting
+// Entry points return 0 on success and a negative code otherwise, after printing the reason:
+// -1 an argument the path does not support (the reference prints and exits, api.cu:205-211),
+// -2 a HIP runtime error.
+#define HI_FAIL(...)                                  \
+  do {                                                \
+    fprintf(stderr, "hipinfer_amd: " __VA_ARGS__);    \
+    fputc('\n', stderr);                              \
+    return -1;                                        \
+  } while (0)
+#define HI_TRY(call)                                                                                 \
+  do {                                                                                               \
+    hipError_t e_ = (call);                                                                          \
+    if (e_ != hipSuccess) {                                                                          \
+      fprintf(stderr, "hipinfer_amd: %s failed: %s (%s:%d)\n", #call, hipGetErrorString(e_), __FILE__, \
+              __LINE__);                                                                             \
+      return -2;                                                                                     \
+    }                                                                                                \
+  } while (0)
+
+// Per-device properties, read once per device (hi_runtime.hip).
+struct HiDevice {
+  int id = -1, cus = 0, lds_max = 0, xcds = 8;
+};
+const HiDevice* hi_device();  // current device; nullptr on a HIP error (already reported)
+// Largest number of resident blocks of `fn` per CU at `block` threads and `lds` dynamic bytes
+// (cached per device and kernel); sets the kernel's dynamic-LDS limit first when lds > 64 KB.
+int hi_blocks_per_cu(const void* fn, int block, size_t lds);
+
+// ------------------------------------------------------------------ device helpers
+// DPP lane moves with compile-time controls (gfx9 encodings): quad_perm, row_half_mirror, row_mirror.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the same total. The tree is fixed
+// (pairs 1, 2, then half-row and row mirrors, then rows 16 and 32 apart), and IEEE addition is
+// commutative, so a value's sum never depends on which lane asks or on how many values the
+// caller reduces.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  v += dpp<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  v = fmaxf(v, __shfl_xor(v, 32, kWave));
+  return v;
+}
+
+// Four int8 weights (one 32-bit word, k order) as two exact fp16 pairs. Each byte, offset by
+// 128, becomes the low mantissa byte of the fp16 1024.0 (0x6400 | b = 1024 + b exactly, one
+// v_perm_b32 builds two halves), and one packed fp16 subtraction of 1152 leaves q exactly
+// (|q| <= 128 is an integer, representable in fp16). Two VALU ops per two weights.
+__device__ __forceinline__ void i8x4_to_f16(uint32_t w, f16x2& lo, f16x2& hi) {
+  const uint32_t b = w ^ 0x80808080u;
+  const uint32_t l = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);  // [b0, 0x64, b1, 0x64]
+  const uint32_t h = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);  // [b2, 0x64, b3, 0x64]
+  const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
+  lo = __builtin_bit_cast(f16x2, l) - bias;
+  hi = __builtin_bit_cast(f16x2, h) - bias;
+}
+
+__device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
+// A 32-bit word as two fp16 values. Always go through this (a scalar parameter): this clang folds
+// __builtin_bit_cast applied directly to a vector element `v[p]` to element 0 of `v`.
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+__device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// HF's act_fn(gate) * up with every step rounded to fp16 (reference src/kernels.cuh:100-105).
+__device__ __forceinline__ f16 silu_mul(float g, float u) {
+  const float gh = (float)(f16)g;
+  const f16 s = (f16)(gh / (1.0f + __expf(-gh)));
+  return s * (f16)u;  // fp16 product, correctly rounded
+}
+
+// One RoPE pair with PyTorch's per-op fp16 rounding (reference src/kernels.cuh:132-136).
+__device__ __forceinline__ void rope_pair(f16& y1, f16& y2, f16x2 cs) {
+  const float c = (float)cs.x, sn = (float)cs.y, f1 = (float)y1, f2 = (float)y2;
+  const f16 a = (f16)((float)(f16)(f1 * c) - (float)(f16)(f2 * sn));
+  const f16 b = (f16)((float)(f16)(f2 * c) + (float)(f16)(f1 * sn));
+  y1 = a;
+  y2 = b;
+}

@@ -1,0 +1,187 @@
+"""ctypes host for libhipinfer.so: the matmul hot path of hipinfer on torch tensors.
+
+Mirrors the kernel-level functions of the reference's scripts/hipinfer.py (gemv, gemv_qkv_rope,
+gemm, moe_router, moe_experts, rmsnorm; hipinfer.py:101-161, 288-306) with the same names,
+arguments and defaults, over the same hi_* C symbols, plus the int8 quantiser of
+scripts/export.py:54-101 (quantize_rows, dequantize_rows, interleave_gate_up) running on the GPU.
+torch is only the container for device memory and the current stream.
+
+Errors: a launcher that rejects its arguments returns a negative code (the reason is printed on
+stderr); these wrappers raise ValueError then. There is no CPU fallback: without the built library
+or a GPU every call fails.
+"""
+import ctypes as C
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = os.environ.get("HIPINFER_LIB", os.path.join(_HERE, "libhipinfer.so"))
+if not os.path.exists(_LIB):
+    raise ImportError(f"hipinfer_amd: {_LIB} is not built; run `python -m hipinfer_amd.build`")
+lib = C.CDLL(os.path.abspath(_LIB))
+
+P, I, F, LL = C.c_void_p, C.c_int, C.c_float, C.c_longlong
+_SIGS = {
+    "hi_rmsnorm": [P, P, P, I, I, F, P],
+    "hi_gemv": [P, I, P, F, P, P, I, I, I, I, I, P],
+    "hi_gemv_w8": [P, I, P, F, P, P, P, I, I, I, I, I, P],
+    "hi_gemv_qkv_rope": [P, I, P, F, P, P, P, I, I, I, I, I, I, P, P, P, P, I, P],
+    "hi_gemv_qkv_rope_w8": [P, I, P, F, P, P, P, P, I, I, I, I, I, I, P, P, P, P, I, P],
+    "hi_quantize_rows": [P, LL, I, P, P, P],
+    "hi_dequantize_rows": [P, P, LL, I, P, P],
+    "hi_device_cus": [],
+}
+_OPTIONAL = {
+    "hi_gemm": [P, I, P, P, P, I, I, I, I, I, P],
+    "hi_gemm_w8": [P, I, P, P, P, P, I, I, I, I, I, P],
+    "hi_gemm_force_config": [I],
+    "hi_gemm_force_splits": [I],
+    "hi_gemm_num_configs": [],
+    "hi_gemm_config_desc": [I, C.c_char_p, I],
+    "hi_moe_router": [P, I, P, I, I, I, I, I, P, P, P],
+    "hi_moe_work_bytes": [I, I, I, I, I],
+    "hi_moe_experts": [P, I, P, P, P, P, I, I, I, I, I, I, F, P, I, I, P, P],
+}
+for _name, _args in list(_SIGS.items()) + [(n, a) for n, a in _OPTIONAL.items() if hasattr(lib, n)]:
+    _fn = getattr(lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = I
+if hasattr(lib, "hi_moe_work_bytes"):
+    lib.hi_moe_work_bytes.restype = C.c_size_t
+MOE_NORM_TOPK, MOE_FP16_WEIGHTS = 1, 2  # moe_flags bits (reference scripts/hipinfer.py:67)
+
+
+def _s():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _p(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _ok(r, what):
+    if r != 0:
+        raise ValueError(f"hipinfer_amd {what}: rejected (code {r}; reason on stderr)")
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("hipinfer_amd: tensors must live on the GPU")
+
+
+# W [N, K]: fp16, or int8 with `scales` [N] fp16 (one per output row: W ~ W_int8 * scales[:, None]).
+def _w8(W, scales):
+    if scales is None:
+        assert W.dtype == torch.float16
+        return False
+    assert W.dtype == torch.int8 and scales.dtype == torch.float16 and scales.shape == (W.shape[0],)
+    return True
+
+
+def rmsnorm(x, w, eps=1e-5):
+    _dev(x, w)
+    y = torch.empty_like(x)
+    _ok(lib.hi_rmsnorm(_p(x), _p(w), _p(y), x.shape[0], x.shape[1], eps, _s()), "rmsnorm")
+    return y
+
+
+def gemv(x, W, out=None, normw=None, eps=1e-5, epi=0, scales=None):
+    """out[M, *] (epi) x[M, K] @ W[N, K]^T for small M; epi 0 store, 1 residual (out += y),
+    2 SwiGLU over gate/up rows interleaved in groups of 16 (out is N/2 wide)."""
+    M, K = x.shape
+    N = W.shape[0]
+    if out is None:
+        out = torch.empty(M, N // 2 if epi == 2 else N, dtype=x.dtype, device=x.device)
+    _dev(x, W, out, normw, scales)
+    if _w8(W, scales):
+        r = lib.hi_gemv_w8(_p(x), x.stride(0), _p(normw), eps, _p(W), _p(scales), _p(out), out.stride(0), M, N, K, epi,
+                           _s())
+    else:
+        r = lib.hi_gemv(_p(x), x.stride(0), _p(normw), eps, _p(W), _p(out), out.stride(0), M, N, K, epi, _s())
+    _ok(r, "gemv")
+    return out
+
+
+def gemv_qkv_rope(x, W, normw, Hq, Hkv, cs, pos, kc, vc, out, bias=None, eps=1e-5, scales=None):
+    """Fused RMSNorm + QKV GEMV (+ bias) + RoPE + KV-cache write. Row m -> cache slot m at pos[m]."""
+    D = kc.shape[-1]
+    _dev(x, W, cs, pos, kc, vc, out, bias, normw, scales)
+    if _w8(W, scales):
+        r = lib.hi_gemv_qkv_rope_w8(_p(x), x.stride(0), _p(normw), eps, _p(W), _p(scales), _p(bias), _p(out),
+                                    out.stride(0), x.shape[0], x.shape[1], Hq, Hkv, D, _p(cs), _p(pos), _p(kc), _p(vc),
+                                    kc.shape[2], _s())
+    else:
+        r = lib.hi_gemv_qkv_rope(_p(x), x.stride(0), _p(normw), eps, _p(W), _p(bias), _p(out), out.stride(0),
+                                 x.shape[0], x.shape[1], Hq, Hkv, D, _p(cs), _p(pos), _p(kc), _p(vc), kc.shape[2], _s())
+    _ok(r, "gemv_qkv_rope")
+    return out
+
+
+def gemm(A, W, out=None, epi=0, bias=None, scales=None):
+    """C (epi) A[M, K] @ W[N, K]^T on the MFMA GEMM (+ bias for epi 0)."""
+    M, K = A.shape
+    N = W.shape[0]
+    if out is None:
+        out = torch.empty(M, N // 2 if epi == 2 else N, dtype=A.dtype, device=A.device)
+    _dev(A, W, out, bias, scales)
+    if _w8(W, scales):
+        r = lib.hi_gemm_w8(_p(A), A.stride(0), _p(W), _p(scales), _p(bias), _p(out), out.stride(0), M, N, K, epi, _s())
+    else:
+        r = lib.hi_gemm(_p(A), A.stride(0), _p(W), _p(bias), _p(out), out.stride(0), M, N, K, epi, _s())
+    _ok(r, "gemm")
+    return out
+
+
+def moe_router(xn, Wr, k, flags):
+    """Top-k experts of each normalised row xn [M, H] under router Wr [E, H]: (idx [M, k] int32,
+    weights [M, k] fp32), descending."""
+    M, H = xn.shape
+    _dev(xn, Wr)
+    idx = torch.empty(M, k, dtype=torch.int32, device=xn.device)
+    w = torch.empty(M, k, dtype=torch.float32, device=xn.device)
+    _ok(lib.hi_moe_router(_p(xn), xn.stride(0), _p(Wr), M, Wr.shape[0], H, k, flags, _p(idx), _p(w), _s()), "moe_router")
+    return idx, w
+
+
+def moe_experts(xn, wgu, wdown, idx, w, x, flags, scale=1.0, path=0):
+    """x += MoE(xn) in place, given the routing: wgu [E, 2I, H] (gate/up interleaved per expert),
+    wdown [E, H, I]. path 0 auto, 1 GEMV, 2 grouped GEMM."""
+    M, H = xn.shape
+    E, I, k = wgu.shape[0], wdown.shape[2], idx.shape[1]
+    _dev(xn, wgu, wdown, idx, w, x)
+    work = torch.empty(lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device=xn.device)
+    _ok(lib.hi_moe_experts(_p(xn), xn.stride(0), _p(wgu), _p(wdown), _p(idx), _p(w), M, E, k, H, I, flags, scale, _p(x),
+                           x.stride(0), path, _p(work), _s()), "moe_experts")
+    return x
+
+
+# ------------------------------------------------------------------ int8 weight format (GPU)
+def quantize_rows(w):
+    """scripts/export.py:54-68 on the GPU, bit-exact: s[n] = fp16(max_k |w[n, k]| / 127),
+    q = clamp(round(w / s), -127, 127), q = 0 for an all-zero row. Returns (q int8, s fp16)."""
+    assert w.dtype == torch.float16 and w.dim() == 2
+    w = w.contiguous()
+    _dev(w)
+    q = torch.empty(w.shape, dtype=torch.int8, device=w.device)
+    s = torch.empty(w.shape[0], dtype=torch.float16, device=w.device)
+    _ok(lib.hi_quantize_rows(_p(w), w.shape[0], w.shape[1], _p(q), _p(s), _s()), "quantize_rows")
+    return q, s
+
+
+def dequantize_rows(q, s):
+    """scripts/export.py:71-73: fp16(q * s), the weights the int8 GEMM computes with."""
+    q = q.contiguous()
+    _dev(q, s)
+    out = torch.empty(q.shape, dtype=torch.float16, device=q.device)
+    _ok(lib.hi_dequantize_rows(_p(q), _p(s), q.shape[0], q.shape[1], _p(out), _s()), "dequantize_rows")
+    return out
+
+
+def interleave_gate_up(gate, up, group=16):
+    """scripts/export.py:97-101: [2I, H] with 16 gate rows, then the same 16 up rows, per group."""
+    inter, hidden = gate.shape
+    g = gate.reshape(inter // group, group, hidden)
+    u = up.reshape(inter // group, group, hidden)
+    return torch.stack([g, u], dim=1).reshape(2 * inter, hidden)

@@ -1,0 +1,64 @@
+/* libhipinfer.so -- MI355X (gfx950) matmul hot path of hipinfer, C ABI.
+ *
+ * Drop-in for the kernel launchers of the reference's src/api.cu that scripts/hipinfer.py binds
+ * over ctypes (argtypes at scripts/hipinfer.py:12-31, 66-71). Same symbol names, argument order
+ * and meaning. Conventions (reference api.cu:18, SURVEYed in hipinfer.py:101-161):
+ *   - every tensor is a caller-owned device pointer; leading dimensions are in elements;
+ *   - fp16 data is IEEE binary16; int8 weights [N, K] carry one fp16 scale per output row
+ *     (W[n, k] ~ q[n, k] * s[n], docs/quantization.md);
+ *   - epi: 0 store (+ bias where a bias argument exists), 1 residual (out += y, fp16 add),
+ *     2 SwiGLU over gate/up rows interleaved in groups of 16 (out is N/2 wide);
+ *   - `stream` is a hipStream_t (torch's current stream); launches are asynchronous.
+ * Return value: 0 on success; -1 when the arguments are outside what the path supports (the
+ * reason is printed on stderr; the reference prints and calls exit(1) there, api.cu:205-211,557);
+ * -2 on a HIP runtime error. ctypes callers that ignore the return value (the reference's
+ * argtypes declare no restype) keep working unchanged.
+ */
+#ifndef HIPINFER_AMD_H
+#define HIPINFER_AMD_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- decode GEMV, M <= 16 rows (M <= 8 with the fused RMSNorm per launch; more rows are chunked) */
+
+/* out[M, *] (epi) x[M, K] @ W[N, K]^T with fp16 W; normw != NULL fuses RMSNorm(x; normw, eps).
+ * Replaces api.cu:181-185 (hi_gemv); binding hipinfer.py:14. */
+int hi_gemv(const void* x, int ldx, const void* normw, float eps, const void* W, void* out, int ldo, int M, int N,
+            int K, int epi, void* stream);
+
+/* The same with int8 W and fp16 row scales [N]. Replaces api.cu:187-191 (hi_gemv_w8); hipinfer.py:17. */
+int hi_gemv_w8(const void* x, int ldx, const void* normw, float eps, const void* W, const void* scales, void* out,
+               int ldo, int M, int N, int K, int epi, void* stream);
+
+/* Fused QKV projection (+ bias) + RoPE + KV-cache write: q to out[m, 0:Hq*D]; k and v to
+ * kc/vc [slots][Hkv][max_seq][D] at slot m, position pos[m]; cs is [max_seq][D/2] (cos, sin) fp16.
+ * Replaces api.cu:216-222 (hi_gemv_qkv_rope); hipinfer.py:16. */
+int hi_gemv_qkv_rope(const void* x, int ldx, const void* normw, float eps, const void* W, const void* bias, void* out,
+                     int ldo, int M, int K, int Hq, int Hkv, int D, const void* cs, const int* pos, void* kc, void* vc,
+                     int max_seq, void* stream);
+
+/* The same with int8 W and row scales. Replaces api.cu:224-230 (hi_gemv_qkv_rope_w8); hipinfer.py:18. */
+int hi_gemv_qkv_rope_w8(const void* x, int ldx, const void* normw, float eps, const void* W, const void* scales,
+                        const void* bias, void* out, int ldo, int M, int K, int Hq, int Hkv, int D, const void* cs,
+                        const int* pos, void* kc, void* vc, int max_seq, void* stream);
+
+/* ---- RMSNorm (unfused form of the GEMV prologue; the reference's tests build references with it)
+ * y[M, H] = w * fp16(x * rsqrt(mean(x^2) + eps)), rows contiguous. Replaces api.cu:76-79
+ * (hi_rmsnorm); hipinfer.py:13. */
+int hi_rmsnorm(const void* x, const void* w, void* y, int M, int H, float eps, void* stream);
+
+/* ---- int8 weight format on the GPU (the reference does this on the host in Python)
+ * q[N, K] int8, s[N] fp16 from fp16 w[N, K], bit-exact with scripts/export.py:54-68 quantize_rows. */
+int hi_quantize_rows(const void* w, long long N, int K, void* q, void* s, void* stream);
+/* out[N, K] = fp16(q * s), bit-exact with scripts/export.py:71-73 dequantize_rows. */
+int hi_dequantize_rows(const void* q, const void* s, long long N, int K, void* out, void* stream);
+
+/* Compute units of the current device (diagnostics; the launchers size their grids from it). */
+int hi_device_cus(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

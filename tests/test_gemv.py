@@ -1,0 +1,251 @@
+"""GPU parity of the decode GEMV and the int8 quantiser, through the C-ABI (hipinfer_amd.hipinfer),
+against the CPU oracle on the same seeded inputs.
+
+Mirrors the reference's tests/test_kernels.py test_gemv (47-65), test_gemv_qkv_rope (264-286),
+test_quantize_rows (364-379) and test_gemv_int8 (382-440): same shapes, row counts and
+tolerances, with the oracle (oracle/hi_oracle.c) in place of torch's fp32 math. Adds the checks
+the MI355X design needs: exact int8 unpacking for every code at every lane position, row
+independence (row m of an M-row GEMV equals the 1-row GEMV bit for bit), the 8-byte int8 path
+(K % 16 == 8), row chunking (M = 16 at large K), strided activations/outputs, and argument
+rejection.
+"""
+import numpy as np
+import pytest
+
+from tests._util import bits, check, cuda, gpu, h16, host, interleave, rng
+
+pytestmark = gpu
+
+
+@pytest.fixture(scope="module")
+def hi():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from hipinfer_amd import hipinfer
+    return hipinfer
+
+
+@pytest.fixture(scope="module")
+def O():
+    from oracle import oracle
+    return oracle
+
+
+def q8(O, W):
+    return O.quantize_rows(W)
+
+
+SHAPES = [(2048, 5632), (896, 4864), (3072, 8192)]
+
+
+@pytest.mark.parametrize("H,I", SHAPES)
+@pytest.mark.parametrize("q", [False, True], ids=["fp16", "int8"])
+def test_gemv_epilogues(hi, O, H, I, q):
+    r = rng(100 + H)
+    for M in [1, 3, 8, 11]:
+        x = h16(r, M, H)
+        W = h16(r, 2560, H, sd=0.02)
+        s = None
+        if q:
+            W, s = q8(O, W)
+        got = host(hi.gemv(cuda(x), cuda(W), scales=None if s is None else cuda(s)))
+        check(f"gemv M={M} K={H}", got, O.gemv(x, W, scales=s), 2e-3, 2e-3)
+        nw = (r.random(H) + 0.5).astype(np.float16)
+        got = host(hi.gemv(cuda(x), cuda(W), normw=cuda(nw), scales=None if s is None else cuda(s)))
+        check(f"gemv+rmsnorm M={M} K={H}", got, O.gemv(x, W, normw=nw, scales=s), 3e-3, 3e-3)
+        res = h16(r, M, H)
+        W2 = h16(r, H, I, sd=0.02)
+        s2 = None
+        if q:
+            W2, s2 = q8(O, W2)
+        a = h16(r, M, I)
+        out = cuda(res)
+        hi.gemv(cuda(a), cuda(W2), out=out, epi=1, scales=None if s2 is None else cuda(s2))
+        check(f"gemv+residual M={M} K={I}", host(out), O.gemv(a, W2, out=res.copy(), epi=1, scales=s2), 4e-3, 2e-3)
+        gu = interleave(h16(r, I, H, sd=0.02), h16(r, I, H, sd=0.02))
+        sg = None
+        if q:
+            gu, sg = q8(O, gu)
+        got = host(hi.gemv(cuda(x), cuda(gu), epi=2, normw=cuda(nw), scales=None if sg is None else cuda(sg)))
+        check(f"gemv+norm+swiglu M={M} I={I}", got, O.gemv(x, gu, epi=2, normw=nw, scales=sg), 3e-3, 3e-3)
+
+
+def test_int8_unpack_every_code_every_position(hi):
+    """Each int8 code at each of the 16 byte positions of a 16-byte load (and across the 64
+    lanes) comes out exactly: s = 1, x = a unit vector -> out[n] = q[n, k]."""
+    import torch
+    K = 64 * 16 * 2
+    q = np.zeros((256, K), np.int8)
+    for v in range(256):
+        q[v, :] = np.int8(((v * 37) % 255) - 127)  # neighbours that must not leak in
+    ks = [0, 1, 2, 3, 5, 8, 13, 15, 16, 17, 1023, 1024, 2047]
+    for k in ks:
+        qq = q.copy()
+        qq[:, k] = (np.arange(256) - 128).astype(np.int8)
+        x = np.zeros((1, K), np.float16)
+        x[0, k] = 1.0
+        out = host(hi.gemv(cuda(x), cuda(qq), scales=torch.ones(256, dtype=torch.float16, device="cuda")))
+        assert np.array_equal(out[0].astype(np.float32), qq[:, k].astype(np.float32)), f"k={k}"
+
+
+def test_fp16_onehot_exact(hi):
+    r = rng(7)
+    K = 4096
+    W = h16(r, 300, K, sd=0.5)
+    for k in [0, 7, 8, 511, 512, 4095]:
+        x = np.zeros((1, K), np.float16)
+        x[0, k] = 1.0
+        assert np.array_equal(bits(host(hi.gemv(cuda(x), cuda(W)))[0]), bits(W[:, k]))
+
+
+@pytest.mark.parametrize("q", [False, True], ids=["fp16", "int8"])
+@pytest.mark.parametrize("norm", [False, True], ids=["plain", "norm"])
+def test_row_independence(hi, O, q, norm):
+    """Row m of an M-row GEMV is bit-identical to the 1-row GEMV of that row (reference
+    api.cu:153-155), for every M the launcher chunks differently."""
+    r = rng(8)
+    H, N = 2048, 1024
+    x = h16(r, 16, H)
+    W = h16(r, N, H, sd=0.02)
+    s = None
+    if q:
+        W, s = q8(O, W)
+    Wd, sd = cuda(W), None if s is None else cuda(s)
+    nw = cuda((r.random(H) + 0.5).astype(np.float16)) if norm else None
+    ones = [host(hi.gemv(cuda(x[m:m + 1]), Wd, normw=nw, scales=sd))[0] for m in range(16)]
+    for M in ([2, 3, 5, 8] if norm else [2, 3, 5, 8, 16]):
+        got = host(hi.gemv(cuda(x[:M]), Wd, normw=nw, scales=sd))
+        for m in range(M):
+            assert np.array_equal(bits(got[m]), bits(ones[m])), f"M={M} row {m}"
+
+
+QKV = [(64, 32, 4, 2048, False), (128, 24, 8, 3072, False), (128, 12, 2, 1536, True), (64, 14, 2, 896, True)]
+
+
+def rope_table(S, D, theta=10000.0):
+    inv = 1.0 / (theta ** (np.arange(0, D, 2, dtype=np.float64) / D))
+    ang = np.arange(S)[:, None] * inv[None, :]
+    return np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float16)  # [S, D/2, 2]
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,H,bias", QKV)
+@pytest.mark.parametrize("q", [False, True], ids=["fp16", "int8"])
+def test_gemv_qkv_rope(hi, O, D, Hq, Hkv, H, bias, q):
+    r = rng(200 + D + Hq)
+    S = 512
+    cs = rope_table(S, D)
+    for M in [1, 3, 8]:
+        x = h16(r, M, H)
+        W = h16(r, (Hq + 2 * Hkv) * D, H, sd=0.02)
+        s = None
+        if q:
+            W, s = q8(O, W)
+        b = h16(r, (Hq + 2 * Hkv) * D) if bias else None
+        nw = (r.random(H) + 0.5).astype(np.float16)
+        pos = r.integers(0, S, M).astype(np.int32)
+        out_r = np.zeros((M, Hq * D), np.float16)
+        kc_r = np.zeros((M, Hkv, S, D), np.float16)
+        vc_r = np.zeros_like(kc_r)
+        O.gemv_qkv_rope(x, W, nw, Hq, Hkv, cs, pos, kc_r, vc_r, out_r, bias=b, scales=s)
+        out = cuda(np.zeros((M, Hq * D), np.float16))
+        kc, vc = cuda(np.zeros_like(kc_r)), cuda(np.zeros_like(vc_r))
+        hi.gemv_qkv_rope(cuda(x), cuda(W), cuda(nw), Hq, Hkv, cuda(cs), cuda(pos), kc, vc, out,
+                         bias=None if b is None else cuda(b), scales=None if s is None else cuda(s))
+        tag = f"D={D} G={Hq // Hkv}{' bias' if bias else ''} M={M}"
+        # the two sums differ in order: allow 1 fp16 ulp before the rotation (reference tolerance)
+        check(f"qkv+rope {tag}: q", host(out), out_r, 2e-2, 2e-3)
+        check(f"qkv+rope {tag}: k cache", host(kc), kc_r, 2e-2, 2e-3)
+        check(f"qkv+rope {tag}: v cache", host(vc), vc_r, 2e-2, 2e-3)
+
+
+def test_quantize_rows_bit_exact(hi, O):
+    """GPU quantiser == oracle == exact-arithmetic golden rows (reference export.py:54-68)."""
+    import os
+    G = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
+    q, s = hi.quantize_rows(cuda(G["quant_w"]))
+    assert np.array_equal(host(q), G["quant_q"]) and np.array_equal(bits(host(s)), bits(G["quant_s"]))
+    assert np.array_equal(bits(host(hi.dequantize_rows(q, s))), bits(G["dequant"]))
+    r = rng(9)
+    for N, K in [(300, 2048), (64, 4100), (17, 7)]:
+        W = h16(r, N, K, sd=0.02)
+        W[min(7, N - 1)] = 0
+        W[0, min(5, K - 1)] = 3.0
+        qg, sg = hi.quantize_rows(cuda(W))
+        qo, so = O.quantize_rows(W)
+        assert np.array_equal(host(qg), qo) and np.array_equal(bits(host(sg)), bits(so)), f"N={N} K={K}"
+        assert np.array_equal(bits(host(hi.dequantize_rows(qg, sg))), bits(O.dequantize_rows(qo, so)))
+
+
+def test_int8_rows_of_8_byte_alignment(hi, O):
+    """K % 16 == 8: rows are only 8-byte aligned, the 8-byte load path runs."""
+    r = rng(10)
+    for K in [8, 24, 1000, 4104]:
+        x = h16(r, 3, K)
+        W, s = q8(O, h16(r, 320, K, sd=0.02))
+        got = host(hi.gemv(cuda(x), cuda(W), scales=cuda(s)))
+        check(f"int8 K={K}", got, O.gemv(x, W, scales=s), 2e-3, 2e-3)
+
+
+def test_strides_chunking_and_odd_sizes(hi, O):
+    import torch
+    r = rng(11)
+    # strided activations and outputs
+    x = h16(r, 5, 1024 + 64)
+    W = h16(r, 777, 1024, sd=0.02)
+    xd = cuda(x)[:, :1024]
+    out = torch.zeros(5, 800, dtype=torch.float16, device="cuda")
+    hi.gemv(xd, cuda(W), out=out[:, :777])
+    check("strided x/out", host(out[:, :777]), O.gemv(np.ascontiguousarray(x[:, :1024]), W), 2e-3, 2e-3)
+    assert not host(out[:, 777:]).any(), "wrote past N"
+    # M = 16 rows at a K where 16 rows exceed LDS: the launcher chunks the rows
+    x = h16(r, 16, 14336)
+    W, s = q8(O, h16(r, 96, 14336, sd=0.02))
+    check("M=16 K=14336 int8", host(hi.gemv(cuda(x), cuda(W), scales=cuda(s))), O.gemv(x, W, scales=s), 2e-3, 2e-3)
+    # minimum K and a single output row
+    x = h16(r, 2, 8)
+    W = h16(r, 1, 8)
+    check("K=8 N=1", host(hi.gemv(cuda(x), cuda(W))), O.gemv(x, W), 2e-3, 2e-3)
+
+
+def test_rejects_bad_arguments(hi):
+    import torch
+    x = torch.zeros(1, 12, dtype=torch.float16, device="cuda")
+    W = torch.zeros(4, 12, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        hi.gemv(x, W)  # K % 8 != 0
+    x = torch.zeros(1, 64, dtype=torch.float16, device="cuda")
+    W = torch.zeros(48, 64, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        hi.gemv(x, W, epi=2)  # SwiGLU needs N % 32 == 0
+    with pytest.raises(ValueError):
+        hi.gemv(x, W, epi=5)
+
+
+def test_full_size_sampled_rows(hi, O):
+    """Llama-3.1-8B gate/up (28672 x 4096, fused norm + SwiGLU) and lm_head-sized shapes at full
+    size: 256 sampled output units checked against the oracle, plus row independence."""
+    import torch
+    r = rng(12)
+    H, I = 4096, 14336
+    g = torch.Generator(device="cuda").manual_seed(12)
+    W = (torch.randn(2 * I, H, generator=g, device="cuda") * 0.02).half()
+    x = h16(r, 1, H)
+    nw = (r.random(H) + 0.5).astype(np.float16)
+    for q in [False, True]:
+        Wd, sd = (W, None) if not q else hi.quantize_rows(W)
+        got = host(hi.gemv(cuda(x), Wd, epi=2, normw=cuda(nw), scales=sd))
+        units = np.sort(r.choice(I, 256, replace=False))
+        rows = np.concatenate([(units // 16) * 32 + units % 16, (units // 16) * 32 + units % 16 + 16])
+        Wh = host(Wd[torch.from_numpy(rows).cuda()])
+        sh = None if sd is None else host(sd[torch.from_numpy(rows).cuda()])
+        # the sampled units as a 256-unit interleaved matrix of their own
+        blk = np.empty((512,) + Wh.shape[1:], Wh.dtype)
+        sblk = None if sh is None else np.empty(512, np.float16)
+        for i in range(256):
+            j = (i // 16) * 32 + i % 16
+            blk[j], blk[j + 16] = Wh[i], Wh[256 + i]
+            if sblk is not None:
+                sblk[j], sblk[j + 16] = sh[i], sh[256 + i]
+        ref = O.gemv(x, blk, epi=2, normw=nw, scales=sblk)
+        check(f"full-size gate/up {'int8' if q else 'fp16'} sampled", got[:, units], ref, 3e-3, 3e-3)
