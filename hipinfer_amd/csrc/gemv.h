@@ -7,8 +7,10 @@
 //  * the block stages the M activation rows in LDS once, RMSNorm'd on the way when normw is
 //    given (fused prologue, HF rounding order);
 //  * each wave owns one output unit at a time (one weight row, or the row pair an epilogue
-//    combines) and streams it with 128-bit loads, lane l taking 16-byte chunks l, l+64, ...,
-//    U loads per row in flight;
+//    combines) and streams it with 128-bit nontemporal loads (the weights are read once), lane l
+//    taking 16-byte chunks l, l+64, ...; the first unit's loads are issued before the activation
+//    prologue and every next unit's before the current unit's reduction, so the prologue and the
+//    reductions hide under weight traffic;
 //  * int8 chunks are unpacked to exact fp16 in registers (v_perm_b32 + one packed fp16 sub per
 //    two weights) and every pair of weights meets its activation pair in one v_dot2_f32_f16
 //    (fp32 accumulate);
@@ -46,37 +48,109 @@ struct GemvArgs {
 template <int WF> struct WLoad { typedef u32x4 T; };
 template <> struct WLoad<WF_I8H> { typedef u32x2 T; };
 
+constexpr int kGemvThreads = 512;              // 8 waves per block
+constexpr int kGemvWaves = kGemvThreads / kWave;
+
 template <int MR, bool NORM, int EPI, int WF>
-__global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
+__global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   constexpr int NR = EPI >= 2 ? 2 : 1;                  // weight rows per output unit
   constexpr int WPL = WF == WF_I8 ? 16 : 8;             // weights per load
   constexpr int XPL = WPL / 8;                          // 16-byte activation chunks per load
   constexpr int WB = WF == WF_F16 ? 16 : WPL;           // bytes per load
-  constexpr int U = WF == WF_I8 ? 4 : 8;                // loads per row in flight
+  constexpr int U = 8 / NR;                             // loads per row per step (128 B per lane)
+  constexpr int XC = MR <= 8 ? (MR <= 4 ? 4 / MR : 1) : 0;  // activation chunks per row held in registers
   typedef typename WLoad<WF>::T LT;
   extern __shared__ u32x4 xs[];                         // [MR][K / 8] activation chunks
-  __shared__ float red[4][MR];
+  __shared__ float red[kGemvWaves][MR];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = a.K, K8 = K >> 3, M = a.M;
+  const int n_units = EPI >= 2 ? a.N / 2 : a.N;
+  const int nload = K / WPL;
+  const int64_t row_bytes = (int64_t)K * (WF == WF_F16 ? 2 : 1);
+  const char* Wb = reinterpret_cast<const char*>(a.W);
+  const int nw = gridDim.x * kGemvWaves;
 
-  // ---- stage the activation rows (rows >= M are zero so no garbage reaches the sums)
+  auto unit_rows = [&](int u, int (&rows)[NR]) {
+    if constexpr (EPI <= 1) {
+      rows[0] = u;
+    } else if constexpr (EPI == 2) {  // gate/up interleaved in groups of 16 rows
+      rows[0] = (u >> 4) * 32 + (u & 15);
+      rows[NR - 1] = rows[0] + 16;
+    } else {  // rows d and d + D/2 of one head
+      const int HD = a.D >> 1;
+      rows[0] = (u / HD) * a.D + u % HD;
+      rows[NR - 1] = rows[0] + HD;
+    }
+  };
+  // One step of a unit: U 16-byte (or 8-byte) chunks of each of its rows, streamed past the
+  // caches (nontemporal: the weights are read exactly once).
+  auto load_step = [&](LT (&wv)[NR][U], const int (&rows)[NR], int base) {
+#pragma unroll
+    for (int i = 0; i < U; i++) {
+      const int c = base + i * 64 + lane;
+#pragma unroll
+      for (int j = 0; j < NR; j++) {
+        if (c < nload)
+          wv[j][i] = __builtin_nontemporal_load(reinterpret_cast<const LT*>(Wb + rows[j] * row_bytes + (int64_t)c * WB));
+        else
+          wv[j][i] = LT{};
+      }
+    }
+  };
+
+  // ---- 1. activation (and norm-weight) chunks into registers, before any weight load, so
+  //         their latency overlaps the first weight step's
+  const bool xreg = XC > 0 && K8 <= XC * kGemvThreads;
+  u32x4 xr[MR][XC > 0 ? XC : 1];
+  u32x4 nr[XC > 0 ? XC : 1];
+  if (xreg) {
+#pragma unroll
+    for (int j = 0; j < XC; j++) {
+      const int c = tid + j * kGemvThreads;
+      if constexpr (NORM) nr[j] = c < K8 ? *reinterpret_cast<const u32x4*>(a.normw + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int m = 0; m < MR; m++)
+        xr[m][j] = (c < K8 && m < M) ? *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // ---- 2. the first step of this wave's first unit
+  LT wv[NR][U];
+  int rows[NR];
+  const int u0 = blockIdx.x * kGemvWaves + wave;
+  bool have = u0 < n_units;
+  if (have) {
+    unit_rows(u0, rows);
+    load_step(wv, rows, 0);
+  }
+  // ---- 3. stage the activation rows in LDS, RMSNorm'd (HF order) when normw is given; rows >= M
+  //         are zero so no garbage reaches the sums
   if constexpr (NORM) {
     float ss[MR];
 #pragma unroll
     for (int m = 0; m < MR; m++) ss[m] = 0.f;
-    for (int i = tid; i < K8; i += 256) {
+    if (xreg) {
 #pragma unroll
-      for (int m = 0; m < MR; m++) {
-        if (m < M) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * i);
+      for (int j = 0; j < XC; j++)
+#pragma unroll
+        for (int m = 0; m < MR; m++)
 #pragma unroll
           for (int p = 0; p < 4; p++) {
-            const f16x2 h = as_h2(v[p]);
+            const f16x2 h = as_h2(xr[m][j][p]);
             ss[m] = dot2(h, h, ss[m]);
           }
-        }
-      }
+    } else {
+      for (int c = tid; c < K8; c += kGemvThreads)
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+          if (m < M) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c);
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+              const f16x2 h = as_h2(v[p]);
+              ss[m] = dot2(h, h, ss[m]);
+            }
+          }
     }
 #pragma unroll
     for (int m = 0; m < MR; m++) ss[m] = wave_sum(ss[m]);
@@ -88,60 +162,64 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
     float r[MR];
 #pragma unroll
     for (int m = 0; m < MR; m++) {
-      const float tot = (red[0][m] + red[1][m]) + (red[2][m] + red[3][m]);
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < kGemvWaves; w++) tot += red[w][m];
       r[m] = 1.0f / __builtin_sqrtf(tot / (float)K + a.eps);
     }
-    for (int i = tid; i < K8; i += 256) {
-      const u32x4 wv = *reinterpret_cast<const u32x4*>(a.normw + 8 * i);
+    auto norm_chunk = [&](u32x4 v, u32x4 wv_, float rm) {
+      u32x4 o;
 #pragma unroll
-      for (int m = 0; m < MR; m++) {
-        u32x4 o = {0u, 0u, 0u, 0u};
-        if (m < M) {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * i);
+      for (int p = 0; p < 4; p++) {
+        const f16x2 xh = as_h2(v[p]), wh = as_h2(wv_[p]);
+        f16x2 y;
+        y.x = wh.x * (f16)((float)xh.x * rm);  // w * fp16(x * r): fp16 product (HF order)
+        y.y = wh.y * (f16)((float)xh.y * rm);
+        o[p] = as_u32(y);
+      }
+      return o;
+    };
+    if (xreg) {
 #pragma unroll
-          for (int p = 0; p < 4; p++) {
-            const f16x2 xh = as_h2(v[p]), wh = as_h2(wv[p]);
-            f16x2 y;
-            y.x = wh.x * (f16)((float)xh.x * r[m]);  // w * fp16(x * r), fp16 product (HF order)
-            y.y = wh.y * (f16)((float)xh.y * r[m]);
-            o[p] = as_u32(y);
-          }
+      for (int j = 0; j < XC; j++) {
+        const int c = tid + j * kGemvThreads;
+        if (c < K8) {
+#pragma unroll
+          for (int m = 0; m < MR; m++) xs[m * K8 + c] = m < M ? norm_chunk(xr[m][j], nr[j], r[m]) : u32x4{0u, 0u, 0u, 0u};
         }
-        xs[m * K8 + i] = o;
+      }
+    } else {
+      for (int c = tid; c < K8; c += kGemvThreads) {
+        const u32x4 wn = *reinterpret_cast<const u32x4*>(a.normw + 8 * c);
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+          xs[m * K8 + c] = m < M ? norm_chunk(*reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c), wn, r[m])
+                                 : u32x4{0u, 0u, 0u, 0u};
       }
     }
   } else {
-    for (int i = tid; i < MR * K8; i += 256) {
-      const int m = i / K8, c = i - m * K8;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (m < M) v = *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c);
-      xs[i] = v;
+    if (xreg) {
+#pragma unroll
+      for (int j = 0; j < XC; j++) {
+        const int c = tid + j * kGemvThreads;
+        if (c < K8) {
+#pragma unroll
+          for (int m = 0; m < MR; m++) xs[m * K8 + c] = xr[m][j];
+        }
+      }
+    } else {
+      for (int i = tid; i < MR * K8; i += kGemvThreads) {
+        const int m = i / K8, c = i - m * K8;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (m < M) v = *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c);
+        xs[i] = v;
+      }
     }
   }
   __syncthreads();
 
-  const int n_units = EPI >= 2 ? a.N / 2 : a.N;
-  const int nload = K / WPL;
-  const int64_t row_bytes = (int64_t)K * (WF == WF_F16 ? 2 : 1);
-  const char* Wb = reinterpret_cast<const char*>(a.W);
-  const int nw = gridDim.x * 4;
-
-  for (int u = blockIdx.x * 4 + wave; u < n_units; u += nw) {
-    int rows[NR];
-    if constexpr (EPI <= 1) {
-      rows[0] = u;
-    } else if constexpr (EPI == 2) {  // gate/up interleaved in groups of 16 rows
-      rows[0] = (u >> 4) * 32 + (u & 15);
-      rows[NR - 1] = rows[0] + 16;
-    } else {  // rows d and d + D/2 of one head
-      const int HD = a.D >> 1;
-      rows[0] = (u / HD) * a.D + u % HD;
-      rows[NR - 1] = rows[0] + HD;
-    }
-    const char* wr[NR];
-#pragma unroll
-    for (int j = 0; j < NR; j++) wr[j] = Wb + rows[j] * row_bytes;
-
+  // ---- 4. stream the units; each unit's next-unit prefetch is issued before its reduction
+  for (int u = u0; u < n_units; u += nw) {
     float acc[NR][MR];
 #pragma unroll
     for (int j = 0; j < NR; j++)
@@ -149,16 +227,8 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       for (int m = 0; m < MR; m++) acc[j][m] = 0.f;
 
     for (int base = 0; base < nload; base += 64 * U) {
-      LT wv[NR][U];
-#pragma unroll
-      for (int i = 0; i < U; i++) {
-        const int c = base + i * 64 + lane;
-#pragma unroll
-        for (int j = 0; j < NR; j++) {
-          if (c < nload) wv[j][i] = *reinterpret_cast<const LT*>(wr[j] + (int64_t)c * WB);
-          else wv[j][i] = LT{};
-        }
-      }
+      if (!have) load_step(wv, rows, base);
+      have = false;
 #pragma unroll
       for (int i = 0; i < U; i++) {
         const int c = base + i * 64 + lane;
@@ -191,6 +261,15 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
       }
     }
 
+    int cur[NR];
+#pragma unroll
+    for (int j = 0; j < NR; j++) cur[j] = rows[j];
+    if (u + nw < n_units) {
+      unit_rows(u + nw, rows);
+      load_step(wv, rows, 0);
+      have = true;
+    }
+
 #pragma unroll
     for (int j = 0; j < NR; j++)
 #pragma unroll
@@ -205,8 +284,8 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
           a1 = acc[NR - 1][m];
         }
       if constexpr (WF != WF_F16) {
-        a0 *= (float)a.scales[rows[0]];
-        a1 *= (float)a.scales[rows[NR - 1]];
+        a0 *= (float)a.scales[cur[0]];
+        a1 *= (float)a.scales[cur[NR - 1]];
       }
       f16* orow = a.out + lane * a.ldo;
       if constexpr (EPI == 0) {
@@ -220,8 +299,8 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a) {
         const int p = a.pos[lane];
         const int slot = a.kv_slot >= 0 ? a.kv_slot : a.slot_base + lane;
         if (a.bias) {
-          a0 += (float)a.bias[rows[0]];
-          a1 += (float)a.bias[rows[NR - 1]];
+          a0 += (float)a.bias[cur[0]];
+          a1 += (float)a.bias[cur[NR - 1]];
         }
         f16 y1 = (f16)a0, y2 = (f16)a1;
         if (head < a.Hq + a.Hkv) rope_pair(y1, y2, a.cs[(int64_t)p * HD + d]);
@@ -244,14 +323,14 @@ int gemv_launch(const GemvArgs& a, hipStream_t s) {
   if (!d) return -2;
   const size_t lds = (size_t)MR * a.K * 2;
   const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MR, NORM, EPI, WF>);
-  const int bpc = hi_blocks_per_cu(fn, 256, lds);
+  const int bpc = hi_blocks_per_cu(fn, kGemvThreads, lds);
   if (bpc < 0) return -2;
   if (bpc == 0) HI_FAIL("gemv: %zu bytes of activation rows do not fit in LDS", lds);
   const int n_units = EPI >= 2 ? a.N / 2 : a.N;
-  const int slots = bpc * d->cus * 4;
+  const int slots = bpc * d->cus * kGemvWaves;
   const int per_wave = (n_units + slots - 1) / slots;
-  const int grid = (n_units + 4 * per_wave - 1) / (4 * per_wave);
-  hipLaunchKernelGGL((gemv_kernel<MR, NORM, EPI, WF>), dim3(grid), dim3(256), lds, s, a);
+  const int grid = (n_units + kGemvWaves * per_wave - 1) / (kGemvWaves * per_wave);
+  hipLaunchKernelGGL((gemv_kernel<MR, NORM, EPI, WF>), dim3(grid), dim3(kGemvThreads), lds, s, a);
   HI_TRY(hipGetLastError());
   return 0;
 }
