@@ -1,0 +1,4 @@
+// GEMM kernel instances for epilogue 1 (one file per epilogue so they compile in parallel).
+#include "gemm.h"
+
+HI_GEMM_DEFINE_RUN(1)

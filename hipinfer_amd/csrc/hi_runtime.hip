@@ -52,16 +52,23 @@ int hi_blocks_per_cu(const void* fn, int block, size_t lds) {
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
   }
-  if (lds > (size_t)d->lds_max) return 0;
+  hipFuncAttributes fa{};
+  hipError_t e = hipFuncGetAttributes(&fa, fn);
+  if (e != hipSuccess) {
+    fprintf(stderr, "hipinfer_amd: hipFuncGetAttributes failed: %s\n", hipGetErrorString(e));
+    return -1;
+  }
+  const size_t dyn_max = (size_t)d->lds_max - fa.sharedSizeBytes;  // static LDS counts against the CU's
+  if (lds > dyn_max) return 0;
   if (lds > 48 * 1024) {
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, d->lds_max);
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn_max);
     if (e != hipSuccess) {
       fprintf(stderr, "hipinfer_amd: hipFuncSetAttribute failed: %s\n", hipGetErrorString(e));
       return -1;
     }
   }
   int n = 0;
-  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, block, lds);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, block, lds);
   if (e != hipSuccess) {
     fprintf(stderr, "hipinfer_amd: occupancy query failed: %s\n", hipGetErrorString(e));
     return -1;

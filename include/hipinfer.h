@@ -44,6 +44,26 @@ int hi_gemv_qkv_rope_w8(const void* x, int ldx, const void* normw, float eps, co
                         const void* bias, void* out, int ldo, int M, int K, int Hq, int Hkv, int D, const void* cs,
                         const int* pos, void* kc, void* vc, int max_seq, void* stream);
 
+/* ---- prefill GEMM (fp16 MFMA, fp32 accumulate); K % 32 == 0, N % 16 == 0 (N % 32 for epi 2)
+ * C[M, *] (epi) A[M, K] @ W[N, K]^T, + bias[N] for epi 0 when bias != NULL. Replaces api.cu:566-571
+ * (hi_gemm); binding hipinfer.py:24. */
+int hi_gemm(const void* A, int lda, const void* W, const void* bias, void* C, int ldc, int M, int N, int K, int epi,
+            void* stream);
+
+/* The same with int8 W and fp16 row scales; W tiles enter the MFMAs as fp16(q * s).
+ * Replaces api.cu:573-577 (hi_gemm_w8); hipinfer.py:19. */
+int hi_gemm_w8(const void* A, int lda, const void* W, const void* scales, const void* bias, void* C, int ldc, int M,
+               int N, int K, int epi, void* stream);
+
+/* Benchmark and test hooks: force a tile config (-1 automatic), force a split-K factor (-1 automatic),
+ * the number of tile configs and a description of one. Replace api.cu:300-305 and 463
+ * (hi_gemm_force_config, hi_gemm_num_configs, hi_gemm_config_desc, hi_gemm_force_splits);
+ * hipinfer.py:22-28. */
+int hi_gemm_force_config(int cfg);
+int hi_gemm_force_splits(int splits);
+int hi_gemm_num_configs(void);
+int hi_gemm_config_desc(int cfg, char* out, int n);
+
 /* ---- RMSNorm (unfused form of the GEMV prologue; the reference's tests build references with it)
  * y[M, H] = w * fp16(x * rsqrt(mean(x^2) + eps)), rows contiguous. Replaces api.cu:76-79
  * (hi_rmsnorm); hipinfer.py:13. */

@@ -1,0 +1,237 @@
+"""GPU parity of the MFMA prefill GEMM through the C-ABI, against the CPU oracle on the same seeded
+inputs.
+
+Mirrors the reference's tests/test_kernels.py test_gemm (134-179), test_gemm_splitk (68-131),
+test_gemm_int8 (443-470) and test_gemm_graph_after_workspace_growth (182-205): every tile config
+(forced through hi_gemm_force_config) and the automatic choice, split-K 2/4/8 at batched-decode M,
+short K (one and two K tiles per split), every epilogue, the partial SwiGLU tile with a sentinel
+row, int8 weights (the oracle computes on fp16(q * s)), and a captured split-K GEMM replayed after
+the workspace grew. Large shapes are checked on sampled rows (rows are computed independently, so
+the oracle's GEMM of those rows is the exact reference for them). Adds bitwise determinism of
+split-K (partials are summed in split order whatever the arrival order).
+"""
+import numpy as np
+import pytest
+
+from tests._util import bits, check, cuda, gpu, h16, host, interleave, rng
+
+pytestmark = gpu
+
+
+@pytest.fixture(scope="module")
+def hi():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from hipinfer_amd import hipinfer
+    yield hipinfer
+    hipinfer.lib.hi_gemm_force_config(-1)
+    hipinfer.lib.hi_gemm_force_splits(-1)
+
+
+@pytest.fixture(scope="module")
+def O():
+    from oracle import oracle
+    return oracle
+
+
+def sample_rows(M, r, n=24):
+    if M <= n:
+        return np.arange(M)
+    return np.unique(np.concatenate([[0, M - 1], r.choice(M, n - 2, replace=False)]))
+
+
+def gemm_check(hi, O, name, A, W, r, epi=0, bias=None, scales=None, res=None, tol=(3e-3, 3e-3)):
+    """Run the GPU GEMM on the full shape; compare sampled rows with the oracle."""
+    import torch
+    M = A.shape[0]
+    out = cuda(res) if res is not None else None
+    got = host(hi.gemm(cuda(A), cuda(W), out=out, epi=epi, bias=None if bias is None else cuda(bias),
+                       scales=None if scales is None else cuda(scales)))
+    rows = sample_rows(M, r)
+    ref = O.gemm(np.ascontiguousarray(A[rows]), W, out=None if res is None else np.ascontiguousarray(res[rows]),
+                 epi=epi, bias=bias, scales=scales)
+    check(name, got[rows], ref, *tol)
+    torch.cuda.synchronize()
+
+
+SHAPES = [(128, 2560, 2048), (77, 2048, 5632), (512, 32000, 2048), (1000, 2048, 2048), (300, 1152, 896),
+          (64, 6144, 4096), (257, 4096, 14336)]
+
+
+@pytest.mark.parametrize("cfg", [-1, 0, 1, 2, 3, 4, 5])
+def test_gemm_configs(hi, O, cfg):
+    r = rng(300 + cfg)
+    hi.lib.hi_gemm_force_config(cfg)
+    try:
+        for M, N, K in SHAPES:
+            A = h16(r, M, K)
+            W = h16(r, N, K, sd=0.02)
+            gemm_check(hi, O, f"gemm cfg={cfg} M={M} N={N} K={K}", A, W, r)
+        M, H, I = 200, 2048, 5632
+        A = h16(r, M, H)
+        W = h16(r, 1152, H, sd=0.02)
+        b = h16(r, 1152)
+        gemm_check(hi, O, f"gemm+bias cfg={cfg}", A, W, r, bias=b)
+        gu = interleave(h16(r, I, H, sd=0.02), h16(r, I, H, sd=0.02))
+        gemm_check(hi, O, f"gemm+swiglu cfg={cfg}", A, gu, r, epi=2, tol=(4e-3, 4e-3))
+        res = h16(r, M, H)
+        a = h16(r, M, I)
+        W2 = h16(r, H, I, sd=0.02)
+        gemm_check(hi, O, f"gemm+residual cfg={cfg}", a, W2, r, epi=1, res=res, tol=(4e-3, 2e-3))
+        # SwiGLU with a partial last column tile: nothing may be written past column I2
+        I2 = 608
+        gu2 = interleave(h16(r, I2, H, sd=0.02), h16(r, I2, H, sd=0.02))
+        buf = np.full((M + 1, I2), 7.0, np.float16)
+        bd = cuda(buf)
+        hi.gemm(cuda(A), cuda(gu2), out=bd[:M], epi=2)
+        got = host(bd)
+        check(f"gemm+swiglu cfg={cfg} I={I2} (partial tile)", got[:M], O.gemm(A, gu2, epi=2), 4e-3, 4e-3)
+        assert (got[M] == 7.0).all(), "wrote past the output"
+    finally:
+        hi.lib.hi_gemm_force_config(-1)
+
+
+def test_gemm_large_prefill_shapes(hi, O):
+    """Llama-3.2-3B prefill shapes at M = 2000 (non-tile-multiple), automatic choice."""
+    r = rng(310)
+    for N, K in [(5120, 3072), (3072, 8192), (16384, 3072)]:
+        A = h16(r, 2000, K)
+        W = h16(r, N, K, sd=0.02)
+        gemm_check(hi, O, f"gemm M=2000 N={N} K={K}", A, W, r)
+
+
+@pytest.mark.parametrize("sp", [2, 4, 8])
+def test_gemm_splitk(hi, O, sp):
+    r = rng(320 + sp)
+    H, I = 2048, 5632
+    hi.lib.hi_gemm_force_splits(sp)
+    try:
+        for M in [9, 32, 64]:
+            x = h16(r, M, H)
+            W = h16(r, 2560, H, sd=0.02)
+            gemm_check(hi, O, f"split={sp} M={M}", x, W, r)
+            b = h16(r, 2560)
+            gemm_check(hi, O, f"split={sp} +bias M={M}", x, W, r, bias=b)
+            res = h16(r, M, H)
+            a = h16(r, M, I)
+            W2 = h16(r, H, I, sd=0.02)
+            gemm_check(hi, O, f"split={sp} +residual M={M}", a, W2, r, epi=1, res=res, tol=(4e-3, 2e-3))
+            gu = interleave(h16(r, I, H, sd=0.02), h16(r, I, H, sd=0.02))
+            gemm_check(hi, O, f"split={sp} +swiglu M={M}", x, gu, r, epi=2, tol=(4e-3, 4e-3))
+    finally:
+        hi.lib.hi_gemm_force_splits(-1)
+
+
+def test_gemm_short_k(hi, O):
+    """One and two K tiles per split (K % 32 is the floor); a split that does not divide the K
+    tiles leaves no empty split."""
+    r = rng(330)
+    try:
+        for cfg in [-1, 0, 1, 5]:
+            hi.lib.hi_gemm_force_config(cfg)
+            for sp in [1, 2]:
+                hi.lib.hi_gemm_force_splits(sp)
+                for M, K in [(300, 32 * sp), (300, 64 * sp), (129, 96), (33, 32)]:
+                    x = h16(r, M, K)
+                    W = h16(r, 1024, K, sd=0.02)
+                    gemm_check(hi, O, f"short-K cfg={cfg} split={sp} M={M} K={K}", x, W, r)
+    finally:
+        hi.lib.hi_gemm_force_config(-1)
+        hi.lib.hi_gemm_force_splits(-1)
+
+
+@pytest.mark.parametrize("cfg", [-1, 0, 1, 2, 3, 4, 5])
+def test_gemm_int8(hi, O, cfg):
+    r = rng(340 + cfg)
+    H, I = 2048, 5632
+    hi.lib.hi_gemm_force_config(cfg)
+    try:
+        for M, N, K in [(128, 2560, 2048), (77, 2048, 5632), (300, 1152, 896), (2000, 3072, 8192), (9, 2560, 2048)]:
+            q, s = O.quantize_rows(h16(r, N, K, sd=0.02))
+            A = h16(r, M, K)
+            gemm_check(hi, O, f"int8 cfg={cfg} M={M} N={N} K={K}", A, q, r, scales=s)
+        M = 200
+        A = h16(r, M, H)
+        q, s = O.quantize_rows(h16(r, 2560, H, sd=0.02))
+        b = h16(r, 2560)
+        gemm_check(hi, O, f"int8+bias cfg={cfg}", A, q, r, bias=b, scales=s)
+        qg, sg = O.quantize_rows(interleave(h16(r, I, H, sd=0.02), h16(r, I, H, sd=0.02)))
+        gemm_check(hi, O, f"int8+swiglu cfg={cfg}", A, qg, r, epi=2, scales=sg, tol=(4e-3, 4e-3))
+        qd, sd = O.quantize_rows(h16(r, H, I, sd=0.02))
+        gemm_check(hi, O, f"int8+residual cfg={cfg}", h16(r, M, I), qd, r, epi=1, scales=sd, res=h16(r, M, H),
+                   tol=(4e-3, 2e-3))
+    finally:
+        hi.lib.hi_gemm_force_config(-1)
+    for sp in [2, 4]:
+        hi.lib.hi_gemm_force_splits(sp)
+        try:
+            for M in [9, 64]:
+                q, s = O.quantize_rows(h16(r, 2560, H, sd=0.02))
+                gemm_check(hi, O, f"int8 split={sp} M={M}", h16(r, M, H), q, r, bias=h16(r, 2560), scales=s)
+        finally:
+            hi.lib.hi_gemm_force_splits(-1)
+
+
+def test_gemm_splitk_deterministic(hi):
+    r = rng(350)
+    A = cuda(h16(r, 64, 4096))
+    W = cuda(h16(r, 3072, 4096, sd=0.02))
+    hi.lib.hi_gemm_force_splits(8)
+    try:
+        a = host(hi.gemm(A, W))
+        for _ in range(3):
+            assert np.array_equal(bits(host(hi.gemm(A, W))), bits(a))
+    finally:
+        hi.lib.hi_gemm_force_splits(-1)
+
+
+def test_gemm_graph_after_workspace_growth(hi, O):
+    """A split-K GEMM captured in a graph keeps the workspace it was captured with: a later, larger
+    split-K GEMM must not free it. The graph is replayed several times with eager work between the
+    replays, and every replay is checked."""
+    import torch
+    r = rng(360)
+    H = 2048
+    hi.lib.hi_gemm_force_splits(4)
+    try:
+        xh = h16(r, 16, H)
+        Wh = h16(r, 2560, H, sd=0.02)
+        x, W = cuda(xh), cuda(Wh)
+        out = torch.empty(16, 2560, dtype=torch.float16, device="cuda")
+        hi.gemm(x, W, out=out)  # eager: sizes the workspace
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            hi.gemm(x, W, out=out)
+        A = cuda(h16(r, 1024, H))
+        W2 = cuda(h16(r, 8192, H, sd=0.02))
+        hi.gemm(A, W2)  # outgrows the workspace
+        del A, W2
+        junk = torch.full((32 << 20,), 1e4, device="cuda")  # may land on a freed workspace
+        ref = O.gemm(xh, Wh)
+        for _ in range(3):
+            out.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            check("split-K graph replay after workspace growth", host(out), ref, 3e-3, 3e-3)
+            hi.gemm(x, W)  # eager split-K work between replays
+            torch.cuda.synchronize()
+        del junk
+    finally:
+        hi.lib.hi_gemm_force_splits(-1)
+
+
+def test_gemm_rejects_bad_shapes(hi):
+    import torch
+    A = torch.zeros(4, 48, dtype=torch.float16, device="cuda")
+    W = torch.zeros(64, 48, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        hi.gemm(A, W)  # K % 32 != 0
+    A = torch.zeros(4, 64, dtype=torch.float16, device="cuda")
+    W = torch.zeros(40, 64, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        hi.gemm(A, W)  # N % 16 != 0
+    W = torch.zeros(48, 64, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        hi.gemm(A, W, epi=2)  # SwiGLU needs N % 32 == 0
