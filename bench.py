@@ -135,6 +135,87 @@ class Model:
         return L
 
 
+# Llama-3.2-3B prefill
+P_H, P_HQ, P_HKV, P_D, P_I, P_L = 3072, 24, 8, 128, 8192, 28
+P_SHAPES = {"qkv": ((P_HQ + 2 * P_HKV) * P_D, P_H), "o": (P_H, P_HQ * P_D), "gate_up": (2 * P_I, P_H),
+            "down": (P_H, P_I)}
+
+
+class PrefillModel:
+    """All 28 layers' projection weights of Llama-3.2-3B (5.6 GB fp16, plus int8 copies), so a
+    step through every layer streams distinct weights like a real prefill chunk."""
+
+    def __init__(self, torch, hi, q8_too=True):
+        self.torch, self.hi = torch, hi
+        g = torch.Generator(device="cuda")
+        g.manual_seed(SEED + 1)
+        self.layers = [{k: torch.empty(*s, dtype=torch.float16, device="cuda").normal_(0.0, 0.02, generator=g)
+                        for k, s in P_SHAPES.items()} for _ in range(P_L)]
+        self.q8 = [{k: hi.quantize_rows(ly[k]) for k in P_SHAPES} for ly in self.layers] if q8_too else None
+        self.gen = g
+
+    def buffers(self, M):
+        t = self.torch
+        x = t.randn(M, P_H, generator=self.gen, device="cuda").half()
+        return {"x": x, "x0": x.clone(), "qkv": t.empty(M, P_SHAPES["qkv"][0], dtype=t.float16, device="cuda"),
+                "act": t.empty(M, P_I, dtype=t.float16, device="cuda")}
+
+    def layer_pass(self, b, q8, kinds=("qkv", "o", "gate_up", "down")):
+        """Every layer's four GEMMs in the engine's order (attn_rows / mlp_rows, api.cu:1668-1718):
+        QKV (store), o_proj + residual (the attention output is stood in by the q columns), gate/up
+        + SwiGLU, down + residual."""
+        hi = self.hi
+        b["x"].copy_(b["x0"])
+        for l in range(P_L):
+            w = (lambda k: (self.layers[l][k], None)) if not q8 else (lambda k: self.q8[l][k])
+            if "qkv" in kinds:
+                W, s = w("qkv")
+                hi.gemm(b["x"], W, out=b["qkv"], scales=s)
+            if "o" in kinds:
+                W, s = w("o")
+                hi.gemm(b["qkv"][:, :P_HQ * P_D], W, out=b["x"], epi=1, scales=s)
+            if "gate_up" in kinds:
+                W, s = w("gate_up")
+                hi.gemm(b["x"], W, out=b["act"], epi=2, scales=s)
+            if "down" in kinds:
+                W, s = w("down")
+                hi.gemm(b["act"], W, out=b["x"], epi=1, scales=s)
+
+
+def prefill_bench(torch, hi, steps, warmup, q8_too):
+    """Per-layer time and TFLOP/s of the four prefill GEMMs at M in {128, 512, 1024}, and of each
+    GEMM kind alone at M = 1024 (the kernel the MFMA roofline is quoted on)."""
+    pm = PrefillModel(torch, hi, q8_too)
+    flops_layer = lambda M: 2.0 * M * sum(N * K for N, K in P_SHAPES.values())
+    res = {"config": "Llama-3.2-3B prefill GEMMs (QKV 5120x3072, o 3072x3072 +res, gate/up 16384x3072 +SwiGLU, "
+                     "down 3072x8192 +res), 28 distinct layers per step", "layers": {}, "kernels_m1024": {}}
+    for q8 in ([False, True] if q8_too else [False]):
+        tag = "int8" if q8 else "fp16"
+        for M in [128, 512, 1024]:
+            b = pm.buffers(M)
+            g = capture(torch, lambda: pm.layer_pass(b, q8))
+            ms, _ = time_graph(torch, g, max(3, steps // 2), warmup)
+            us = ms * 1e3 / P_L
+            res["layers"][f"M{M}_{tag}"] = {"us_per_layer": round(us, 2),
+                                            "TFLOP/s": round(flops_layer(M) / (us * 1e-6) / 1e12, 1),
+                                            "pct_mfma_peak": round(100 * flops_layer(M) / (us * 1e-6) / 1e12
+                                                                   / MFMA_F16_PEAK_TFLOPS, 1)}
+            del g
+        b = pm.buffers(1024)
+        for kind in P_SHAPES:
+            g = capture(torch, lambda: pm.layer_pass(b, q8, kinds=(kind,)))
+            ms, _ = time_graph(torch, g, max(3, steps // 2), warmup)
+            us = ms * 1e3 / P_L
+            N, K = P_SHAPES[kind]
+            tf = 2.0 * 1024 * N * K / (us * 1e-6) / 1e12
+            res["kernels_m1024"][f"{kind}_{tag}"] = {"N": N, "K": K, "us": round(us, 2), "TFLOP/s": round(tf, 1),
+                                                     "pct_mfma_peak": round(100 * tf / MFMA_F16_PEAK_TFLOPS, 1)}
+            del g
+    del pm
+    torch.cuda.empty_cache()
+    return res
+
+
 def capture(torch, fn):
     fn()  # eager warm-up: per-kernel attributes and occupancy are set outside capture
     torch.cuda.synchronize()
@@ -210,7 +291,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-int8", action="store_true")
-    ap.add_argument("--profile", choices=["gate_up", "token"], default=None,
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM (C3) section")
+    ap.add_argument("--profile", choices=["gate_up", "token", "gemm"], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -230,7 +312,12 @@ def main():
     log(f"weights ready in {time.perf_counter() - t0:.1f} s")
 
     if args.profile:
-        fn = (lambda: model.one_kind("gate_up", False)) if args.profile == "gate_up" else (lambda: model.token(False))
+        if args.profile == "gemm":
+            pm = PrefillModel(torch, hi, False)
+            b = pm.buffers(1024)
+            fn = lambda: pm.layer_pass(b, False)
+        else:
+            fn = (lambda: model.one_kind("gate_up", False)) if args.profile == "gate_up" else (lambda: model.token(False))
         g = capture(torch, fn)
         for _ in range(args.steps):
             g.replay()
@@ -298,6 +385,12 @@ def main():
                        "pct_hbm_peak": round(100 * v8 / HBM_PEAK_GBS, 2), "weight_bytes_per_step": wb8}
     res["kernels"] = kernels
     res["roofline"] = roofline
+    if not args.no_gemm:
+        del g16
+        if "int8" in out:
+            del g8
+        log("prefill GEMM ...")
+        res["prefill_gemm"] = prefill_bench(torch, hi, args.steps, args.warmup, not args.no_int8)
     if not args.no_cpu:
         log("cpu baseline ...")
         res["cpu_baseline"] = cpu_baseline(torch, model)

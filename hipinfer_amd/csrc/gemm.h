@@ -7,16 +7,20 @@
 //  * a block of 4 waves owns a BM x BN output tile; each wave a (BM/WM) x (BN/WN) sub-tile built
 //    from v_mfma_f32_32x32x16_f16 tiles (A and W are both K-contiguous, so each lane's 8-half
 //    fragment is one 16-byte LDS read);
-//  * K advances in 64-deep tiles, double-buffered in LDS: the next tile's global loads are in
-//    flight (in registers) while the MFMAs consume the current one; one barrier per K tile;
-//  * LDS rows hold 8 chunks of 16 bytes whose position is XOR-swizzled by the row (chunk ^ row % 8),
-//    so the 32 rows an MFMA fragment read touches spread over the banks;
-//  * int8 weights are dequantised on their way into LDS: exact int8 -> fp16 unpack, then one
-//    packed fp16 multiply by the row scale = fp16(q * s), the weight the reference's int8 GEMM
-//    computes with (kernels.cuh:86-94, 336-341);
-//  * the tile index is remapped so that the 8 XCDs (blocks are dealt round-robin across them)
-//    each get a contiguous run of tiles, rasterised in groups of 8 tile rows, so the A and W
-//    panels a run needs stay in that XCD's L2;
+//  * K advances in 64-deep tiles through an S-stage ring in LDS fed by gfx950's direct
+//    global->LDS loads (global_load_lds_dwordx4): no register staging, S-1 tiles in flight while
+//    the MFMAs consume the oldest, one explicit vmcnt wait and one barrier per K tile;
+//  * LDS rows hold 16-byte chunks whose position is XOR-swizzled by the row, so the 32 rows one
+//    fragment read touches spread over the banks; the swizzle is applied on the global side (each
+//    lane fetches the chunk that belongs at its LDS slot), since a DMA lane's LDS slot is fixed;
+//  * int8 weights travel to LDS raw (half the bytes) and are dequantised per fragment: exact
+//    int8 -> fp16 unpack, then one packed fp16 multiply by the row scale = fp16(q * s), the weight
+//    the reference's int8 GEMM computes with (kernels.cuh:86-94, 336-341);
+//  * rows past M or N load a clamped (valid) row whose results are never stored; a K tail of 32
+//    skips the last two 16-deep MFMA steps;
+//  * the tile index is remapped so each of the 8 XCDs (blocks are dealt round-robin across them)
+//    gets a contiguous run of tiles, rasterised in groups of 8 tile rows, so the A and W panels a
+//    run needs stay in that XCD's L2;
 //  * epilogues (reference kernels.cuh:454-505): 0 store (+ bias, fp32 before the rounding),
 //    1 residual (fp16 add), 2 SwiGLU over 16-column gate/up groups (the partner column sits 16
 //    lanes away in the MFMA result and is fetched with one lane swizzle);
@@ -42,22 +46,42 @@ struct GemmArgs {
 
 constexpr int kGemmBK = 64;
 constexpr int kGemmThreads = 256;
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-// element (r, k) of an LDS tile with kGemmBK halves per row, 16-byte chunks XOR-swizzled by row
-__device__ __forceinline__ int lds_off(int r, int chunk) { return r * kGemmBK + ((chunk ^ (r & 7)) << 3); }
+// Wait until at most N vector-memory operations (global loads, LDS DMA) are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Workgroup barrier without a memory fence (a fence would drain every in-flight LDS DMA); the
+// DMA completions it orders are waited for explicitly with wait_vmcnt.
+__device__ __forceinline__ void barrier_no_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
-template <int BM, int BN, int WM, int WN, int EPI, bool Q8>
+// Half offset of 16-byte chunk `c` of row `r` in an LDS tile of 64-half (128-byte) rows.
+__device__ __forceinline__ int lds_off(int r, int c) { return r * kGemmBK + ((c ^ (r & 7)) << 3); }
+// Byte offset of 16-byte chunk `c` of row `r` in an LDS tile of 64-byte int8 rows.
+__device__ __forceinline__ int lds_off8(int r, int c) { return r * 64 + ((c ^ (r & 3)) << 4); }
+
+template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8>
 __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
-  constexpr int TM = BM / WM, TN = BN / WN;       // wave tile
-  constexpr int FM = TM / 32, FN = TN / 32;       // MFMA tiles per wave
-  constexpr int CH = kGemmBK / 8;                 // 16-byte chunks per LDS row
-  constexpr int A_PT = BM * CH / kGemmThreads;    // A chunks per thread per K tile
-  constexpr int B_PT = Q8 ? BN * (kGemmBK / 16) / kGemmThreads : BN * CH / kGemmThreads;
+  constexpr int TM = BM / WM, TN = BN / WN;          // wave tile
+  constexpr int FM = TM / 32, FN = TN / 32;          // MFMA tiles per wave
+  constexpr int A_ST = BM * kGemmBK;                 // halves per stage
+  constexpr int B_ROWB = Q8 ? 64 : 128;              // bytes of one W row per K tile
+  constexpr int B_ST = BN * B_ROWB / 2;              // halves per stage
+  constexpr int A_LD = BM / 32;                      // 1 KB DMA instructions per wave per K tile (A)
+  constexpr int B_LD = BN * B_ROWB / 4096;           // ... (W)
+  constexpr int L = A_LD + B_LD;                     // vector-memory ops per lane per K tile
   static_assert(WM * WN == 4 && FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tiling");
-  static_assert(A_PT >= 1 && B_PT >= 1, "tile too small for the block");
+  static_assert(A_LD >= 1 && B_LD >= 1 && (S - 2) * L < 64 && S >= 2 && S <= 4, "pipeline shape");
   extern __shared__ f16 smem[];
-  f16* As = smem;                     // [2][BM][BK]
-  f16* Bs = smem + 2 * BM * kGemmBK;  // [2][BN][BK]
+  f16* As = smem;               // [S][BM][64]
+  f16* Bs = smem + S * A_ST;    // [S][BN][64] fp16, or [S][BN][64 bytes] int8
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -83,79 +107,51 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
 
   const int nkt = (K + kGemmBK - 1) / kGemmBK;
   const int kt0 = blockIdx.y * g.kt_per_split;
-  const int kt1 = min(nkt, kt0 + g.kt_per_split);
+  const int nloc = min(nkt, kt0 + g.kt_per_split) - kt0;  // K tiles of this split
 
-  // ---- global -> register staging
-  u32x4 ra[A_PT];
-  u32x4 rb[B_PT];
-  f16 bscale[B_PT];
+  // ---- DMA of one K tile into stage st. Lane l of an instruction covering 8 (A, W fp16) or
+  //      16 (W int8) rows fills LDS slot l: it fetches the chunk the swizzle puts there.
   const char* Wb = reinterpret_cast<const char*>(g.W);
+  auto issue = [&](int kt, int st) {
+    const int k0 = kt * kGemmBK;
+    f16* as = As + st * A_ST;
 #pragma unroll
-  for (int i = 0; i < B_PT; i++) {
-    bscale[i] = (f16)0.f;
+    for (int i = 0; i < A_LD; i++) {
+      const int r0 = (wave * A_LD + i) * 8, r = r0 + (lane >> 3), lc = (lane & 7) ^ (lane >> 3);
+      const int row = min(bm + r, M - 1);
+      const int k = k0 + lc * 8 < K ? k0 + lc * 8 : k0;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g.A + row * g.lda + k),
+                                       (lds_void_t*)(as + r0 * kGemmBK), 16, 0, 0);
+    }
+    f16* bs = Bs + st * B_ST;
+#pragma unroll
+    for (int i = 0; i < B_LD; i++) {
+      if constexpr (Q8) {
+        const int r0 = (wave * B_LD + i) * 16, r = r0 + (lane >> 2), lc = (lane & 3) ^ (r & 3);
+        const int row = min(bn + r, N - 1);
+        const int k = k0 + lc * 16 < K ? k0 + lc * 16 : k0;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(Wb + (int64_t)row * K + k),
+                                         (lds_void_t*)(reinterpret_cast<char*>(bs) + r0 * 64), 16, 0, 0);
+      } else {
+        const int r0 = (wave * B_LD + i) * 8, r = r0 + (lane >> 3), lc = (lane & 7) ^ (lane >> 3);
+        const int row = min(bn + r, N - 1);
+        const int k = k0 + lc * 8 < K ? k0 + lc * 8 : k0;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(Wb + ((int64_t)row * K + k) * 2),
+                                         (lds_void_t*)(bs + r0 * kGemmBK), 16, 0, 0);
+      }
+    }
+  };
+
+  const int fr = lane & 31, fk = lane >> 5;  // fragment row (or column) and k half
+  f16x2 bsc[FN];                             // int8: the scale of the W row each B fragment reads
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    bsc[j] = f16x2{(f16)0.f, (f16)0.f};
     if constexpr (Q8) {
-      const int c = tid + i * kGemmThreads, r = c / (kGemmBK / 16);
-      if (bn + r < N) bscale[i] = g.scales[bn + r];
+      const f16 sv = g.scales[min(bn + wn * TN + j * 32 + fr, N - 1)];
+      bsc[j] = f16x2{sv, sv};
     }
   }
-  auto gload = [&](int kt) {
-    const int k0 = kt * kGemmBK;
-#pragma unroll
-    for (int i = 0; i < A_PT; i++) {
-      const int c = tid + i * kGemmThreads, r = c / CH, kc = (c % CH) * 8;
-      const int row = bm + r, k = k0 + kc;
-      ra[i] = (row < M && k < K) ? *reinterpret_cast<const u32x4*>(g.A + row * g.lda + k) : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int i = 0; i < B_PT; i++) {
-      if constexpr (Q8) {  // 16 int8 weights per load
-        const int c = tid + i * kGemmThreads, r = c / (kGemmBK / 16), kc = (c % (kGemmBK / 16)) * 16;
-        const int row = bn + r, k = k0 + kc;
-        rb[i] = (row < N && k < K) ? *reinterpret_cast<const u32x4*>(Wb + (int64_t)row * K + k) : u32x4{0u, 0u, 0u, 0u};
-      } else {
-        const int c = tid + i * kGemmThreads, r = c / CH, kc = (c % CH) * 8;
-        const int row = bn + r, k = k0 + kc;
-        rb[i] = (row < N && k < K) ? *reinterpret_cast<const u32x4*>(Wb + ((int64_t)row * K + k) * 2)
-                                   : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-  auto sstore = [&](int st) {
-    f16* as = As + st * BM * kGemmBK;
-    f16* bs = Bs + st * BN * kGemmBK;
-#pragma unroll
-    for (int i = 0; i < A_PT; i++) {
-      const int c = tid + i * kGemmThreads, r = c / CH, ch = c % CH;
-      *reinterpret_cast<u32x4*>(as + lds_off(r, ch)) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_PT; i++) {
-      if constexpr (Q8) {
-        const int c = tid + i * kGemmThreads, r = c / (kGemmBK / 16), ch = (c % (kGemmBK / 16)) * 2;
-        const f16x2 s2 = {bscale[i], bscale[i]};
-        u32x4 lo, hi;
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-          f16x2 a, b;
-          i8x4_to_f16(rb[i][p], a, b);
-          a = a * s2;  // fp16(q * s), one rounding
-          b = b * s2;
-          if (p < 2) {
-            lo[2 * p] = as_u32(a);
-            lo[2 * p + 1] = as_u32(b);
-          } else {
-            hi[2 * p - 4] = as_u32(a);
-            hi[2 * p - 3] = as_u32(b);
-          }
-        }
-        *reinterpret_cast<u32x4*>(bs + lds_off(r, ch)) = lo;
-        *reinterpret_cast<u32x4*>(bs + lds_off(r, ch + 1)) = hi;
-      } else {
-        const int c = tid + i * kGemmThreads, r = c / CH, ch = c % CH;
-        *reinterpret_cast<u32x4*>(bs + lds_off(r, ch)) = rb[i];
-      }
-    }
-  };
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -165,32 +161,52 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  if (kt0 < kt1) {
-    gload(kt0);
-    sstore(0);
-  }
-  __syncthreads();
-  const int fr = lane & 31, fk = lane >> 5;  // fragment row (or column) and k half
-  for (int kt = kt0; kt < kt1; kt++) {
-    const int st = (kt - kt0) & 1;
-    if (kt + 1 < kt1) gload(kt + 1);
-    const f16* as = As + st * BM * kGemmBK;
-    const f16* bs = Bs + st * BN * kGemmBK;
+#pragma unroll
+  for (int s = 0; s < S - 1; s++)
+    if (s < nloc) issue(kt0 + s, s);
+
+  for (int t = 0; t < nloc; t++) {
+    // tile t has landed once at most `later` tiles' DMA remain outstanding
+    const int later = min(S - 2, nloc - 1 - t);
+    if (later >= 2) wait_vmcnt<2 * L>();
+    else if (later == 1) wait_vmcnt<L>();
+    else wait_vmcnt<0>();
+    barrier_no_fence();  // every lane's part of tile t is in LDS; every wave is done with tile t-1
+    if (t + S - 1 < nloc) issue(kt0 + t + S - 1, (t + S - 1) % S);
+
+    const int st = t % S, k0 = (kt0 + t) * kGemmBK;
+    const f16* as = As + st * A_ST;
+    const f16* bs = Bs + st * B_ST;
 #pragma unroll
     for (int ks = 0; ks < kGemmBK / 16; ks++) {
-      const int ch = ks * 2 + fk;
-      f16x8 af[FM], bf[FN];
+      if (k0 + ks * 16 < K) {
+        const int ch = ks * 2 + fk;
+        f16x8 af[FM], bf[FN];
 #pragma unroll
-      for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const f16x8*>(as + lds_off(wm * TM + i * 32 + fr, ch));
+        for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const f16x8*>(as + lds_off(wm * TM + i * 32 + fr, ch));
 #pragma unroll
-      for (int j = 0; j < FN; j++) bf[j] = *reinterpret_cast<const f16x8*>(bs + lds_off(wn * TN + j * 32 + fr, ch));
+        for (int j = 0; j < FN; j++) {
+          if constexpr (Q8) {
+            const int r = wn * TN + j * 32 + fr;
+            const u32x2 q = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(bs) + lds_off8(r, ks) + 8 * fk);
+            f16x2 p0, p1, p2, p3;
+            i8x4_to_f16(q[0], p0, p1);
+            i8x4_to_f16(q[1], p2, p3);
+            p0 = p0 * bsc[j];  // fp16(q * s), one rounding each
+            p1 = p1 * bsc[j];
+            p2 = p2 * bsc[j];
+            p3 = p3 * bsc[j];
+            bf[j] = f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+          } else {
+            bf[j] = *reinterpret_cast<const f16x8*>(bs + lds_off(wn * TN + j * 32 + fr, ch));
+          }
+        }
 #pragma unroll
-      for (int i = 0; i < FM; i++)
+        for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < FN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      }
     }
-    if (kt + 1 < kt1) sstore(st ^ 1);
-    __syncthreads();
   }
 
   // ---- split-K: partial to the workspace; the last block of the tile reduces in split order
@@ -258,24 +274,27 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
     }
 }
 
-// Tile configurations (all 4 waves, BK = 64): {BM, BN, WM, WN}.
+// Tile configurations (all 4 waves, BK = 64): {BM, BN, WM, WN, stages}.
 struct GemmCfg {
-  int bm, bn, wm, wn;
+  int bm, bn, wm, wn, st;
 };
-constexpr GemmCfg kGemmCfgs[] = {{256, 128, 2, 2}, {128, 128, 2, 2}, {128, 64, 2, 2},
-                                 {64, 128, 2, 2},  {64, 64, 2, 2},   {32, 128, 1, 4}};
+constexpr GemmCfg kGemmCfgs[] = {{256, 128, 2, 2, 3}, {128, 128, 2, 2, 4}, {128, 64, 2, 2, 4}, {64, 128, 2, 2, 4},
+                                 {64, 64, 2, 2, 4},   {32, 128, 1, 4, 4},  {256, 256, 2, 2, 2}};
 constexpr int kGemmNumCfgs = sizeof(kGemmCfgs) / sizeof(kGemmCfgs[0]);
-inline size_t gemm_lds_bytes(int cfg) { return (size_t)2 * (kGemmCfgs[cfg].bm + kGemmCfgs[cfg].bn) * kGemmBK * 2; }
+inline size_t gemm_lds_bytes(int cfg, bool q8) {
+  const GemmCfg& c = kGemmCfgs[cfg];
+  return (size_t)c.st * (c.bm * kGemmBK * 2 + c.bn * (q8 ? 64 : 128));
+}
 
-template <int BM, int BN, int WM, int WN, int EPI, bool Q8>
-int gemm_launch(const GemmArgs& g, int splits, hipStream_t s) {
-  const size_t lds = (size_t)2 * (BM + BN) * kGemmBK * 2;
-  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WM, WN, EPI, Q8>);
+template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8>
+int gemm_launch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
+  const size_t lds = gemm_lds_bytes(cfg, Q8);
+  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WM, WN, S, EPI, Q8>);
   const int bpc = hi_blocks_per_cu(fn, kGemmThreads, lds);  // also lifts the dynamic-LDS limit
   if (bpc < 0) return -2;
   if (bpc == 0) HI_FAIL("gemm: tile %dx%d does not fit on a CU", BM, BN);
   const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, EPI, Q8>), dim3(tiles, splits), dim3(kGemmThreads), lds, s, g);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, EPI, Q8>), dim3(tiles, splits), dim3(kGemmThreads), lds, s, g);
   HI_TRY(hipGetLastError());
   return 0;
 }
@@ -287,30 +306,29 @@ int gemm_run(const GemmArgs& g, int cfg, int splits, bool q8, hipStream_t s);
 template <int EPI>
 int gemm_blocks_per_cu(int cfg, bool q8);
 
-#define HI_GEMM_CFG(i, q)                                                                              \
-  if (cfg == i && q8 == q)                                                                             \
-    return gemm_launch<kGemmCfgs[i].bm, kGemmCfgs[i].bn, kGemmCfgs[i].wm, kGemmCfgs[i].wn, EPI, q>(g, splits, s);
-#define HI_GEMM_DEFINE_RUN(EPIV)                                                                       \
-  template <>                                                                                          \
-  int gemm_run<EPIV>(const GemmArgs& g, int cfg, int splits, bool q8, hipStream_t s) {                \
-    constexpr int EPI = EPIV;                                                                          \
-    HI_GEMM_CFG(0, false) HI_GEMM_CFG(1, false) HI_GEMM_CFG(2, false) HI_GEMM_CFG(3, false)            \
-    HI_GEMM_CFG(4, false) HI_GEMM_CFG(5, false)                                                        \
-    HI_GEMM_CFG(0, true) HI_GEMM_CFG(1, true) HI_GEMM_CFG(2, true) HI_GEMM_CFG(3, true)                \
-    HI_GEMM_CFG(4, true) HI_GEMM_CFG(5, true)                                                          \
-    HI_FAIL("gemm: no kernel for config %d", cfg);                                                     \
-  }                                                                                                    \
-  template <>                                                                                          \
-  int gemm_blocks_per_cu<EPIV>(int cfg, bool q8) {                                                     \
-    constexpr int EPI = EPIV;                                                                          \
-    HI_GEMM_OCC(0) HI_GEMM_OCC(1) HI_GEMM_OCC(2) HI_GEMM_OCC(3) HI_GEMM_OCC(4) HI_GEMM_OCC(5)            \
-    return -1;                                                                                         \
-  }
-#define HI_GEMM_OCC(i)                                                                                 \
-  if (cfg == i) {                                                                                      \
-    const void* fn = q8 ? reinterpret_cast<const void*>(&gemm_kernel<kGemmCfgs[i].bm, kGemmCfgs[i].bn,  \
-                                                                      kGemmCfgs[i].wm, kGemmCfgs[i].wn, EPI, true>) \
-                        : reinterpret_cast<const void*>(&gemm_kernel<kGemmCfgs[i].bm, kGemmCfgs[i].bn,  \
-                                                                      kGemmCfgs[i].wm, kGemmCfgs[i].wn, EPI, false>); \
-    return hi_blocks_per_cu(fn, kGemmThreads, gemm_lds_bytes(i));                                      \
+#define HI_GEMM_K(i, q) gemm_kernel<kGemmCfgs[i].bm, kGemmCfgs[i].bn, kGemmCfgs[i].wm, kGemmCfgs[i].wn, kGemmCfgs[i].st, EPI, q>
+#define HI_GEMM_CFG(i, q)                                                                                      \
+  if (cfg == i && q8 == q)                                                                                     \
+    return gemm_launch<kGemmCfgs[i].bm, kGemmCfgs[i].bn, kGemmCfgs[i].wm, kGemmCfgs[i].wn, kGemmCfgs[i].st, EPI, q>( \
+        g, cfg, splits, s);
+#define HI_GEMM_OCC(i)                                                                                         \
+  if (cfg == i)                                                                                                \
+    return hi_blocks_per_cu(q8 ? reinterpret_cast<const void*>(&HI_GEMM_K(i, true))                            \
+                               : reinterpret_cast<const void*>(&HI_GEMM_K(i, false)),                          \
+                            kGemmThreads, gemm_lds_bytes(i, q8));
+#define HI_GEMM_DEFINE_RUN(EPIV)                                                                               \
+  template <>                                                                                                  \
+  int gemm_run<EPIV>(const GemmArgs& g, int cfg, int splits, bool q8, hipStream_t s) {                        \
+    constexpr int EPI = EPIV;                                                                                  \
+    HI_GEMM_CFG(0, false) HI_GEMM_CFG(1, false) HI_GEMM_CFG(2, false) HI_GEMM_CFG(3, false)                    \
+    HI_GEMM_CFG(4, false) HI_GEMM_CFG(5, false) HI_GEMM_CFG(6, false)                                          \
+    HI_GEMM_CFG(0, true) HI_GEMM_CFG(1, true) HI_GEMM_CFG(2, true) HI_GEMM_CFG(3, true)                        \
+    HI_GEMM_CFG(4, true) HI_GEMM_CFG(5, true) HI_GEMM_CFG(6, true)                                             \
+    HI_FAIL("gemm: no kernel for config %d", cfg);                                                             \
+  }                                                                                                            \
+  template <>                                                                                                  \
+  int gemm_blocks_per_cu<EPIV>(int cfg, bool q8) {                                                             \
+    constexpr int EPI = EPIV;                                                                                  \
+    HI_GEMM_OCC(0) HI_GEMM_OCC(1) HI_GEMM_OCC(2) HI_GEMM_OCC(3) HI_GEMM_OCC(4) HI_GEMM_OCC(5) HI_GEMM_OCC(6)    \
+    return -1;                                                                                                 \
   }

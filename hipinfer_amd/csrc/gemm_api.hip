@@ -10,8 +10,12 @@
 // costs its tile's MFMA work divided by that tile's measured efficiency, and split-K pays for its
 // fp32 partial round trip. Split-K workspace is grown only outside stream capture and never freed
 // while the process runs, so a captured graph keeps a valid pointer (reference api.cu:54-73).
+#include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <map>
 #include <mutex>
+#include <tuple>
 #include <vector>
 
 #include "gemm.h"
@@ -46,27 +50,33 @@ int cfg_blocks_per_cu(int cfg, bool q8) {
 }
 
 // Relative MFMA efficiency of each tile shape (bigger tiles reuse more of what they stage).
-constexpr double kCfgEff[kGemmNumCfgs] = {1.0, 0.85, 0.7, 0.7, 0.5, 0.45};
+constexpr double kCfgEff[kGemmNumCfgs] = {1.0, 0.85, 0.7, 0.7, 0.5, 0.45, 1.0};
 
 struct Choice {
   int cfg, splits;
 };
 
+// Fallback model (stream capture, autotuning off): rounds of resident blocks times the tile's
+// MFMA time at its efficiency, or the L2/MALL time of everything the tiles stage, whichever is
+// longer, plus the split-K partial round trip.
 Choice gemm_pick(int M, int N, int K, bool q8, int cus) {
   Choice best{1, 1};
   double best_t = 1e300;
   const int nkt = (K + kGemmBK - 1) / kGemmBK;
+  const double mfma_per_cu = 4069.0 * 2.4e9;  // fp16 flop/s per CU at the datasheet peak
+  const double l2_bw = 20e12;                 // aggregate L2/MALL bytes/s the staging can draw
   for (int c = 0; c < kGemmNumCfgs; c++) {
     const int bm = kGemmCfgs[c].bm, bn = kGemmCfgs[c].bn;
     const double tiles = (double)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int slots = cus * cfg_blocks_per_cu(c, q8);
-    for (int sp = 1; sp <= 16; sp *= 2) {
-      if (sp > nkt || (sp > 1 && tiles * sp > 8.0 * cus) || tiles > kMaxTiles) continue;
+    for (int sp = 1; sp <= 8; sp *= 2) {
+      if (sp > nkt || (sp > 1 && tiles * sp > 4.0 * cus) || tiles > kMaxTiles) continue;
       const int kps = (nkt + sp - 1) / sp;
       const double rounds = std::ceil(tiles * sp / slots);
-      double t = rounds * (double)bm * bn * kps * kGemmBK / kCfgEff[c];
-      if (sp > 1) t += tiles * sp * bm * bn * 24.0;  // partial write + read back, per element
-      t += (double)bm * bn * kGemmBK * 2.0;          // prologue / epilogue per round
+      const double t_mfma = rounds * 2.0 * bm * bn * kps * kGemmBK / (mfma_per_cu * kCfgEff[c]);
+      const double t_l2 = tiles * sp * kps * (double)(bm * 128 + bn * (q8 ? 64 : 128)) / l2_bw;
+      double t = std::max(t_mfma, t_l2) + 2e-6;
+      if (sp > 1) t += tiles * sp * bm * bn * 8.0 / 4e12 + 2e-6;
       if (t < best_t) {
         best_t = t;
         best = {c, sp};
@@ -107,6 +117,137 @@ int ensure_ws(size_t bytes, hipStream_t s, bool* ok) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s);
+
+// First-call autotuning per (M bucket, N, K, SwiGLU, int8) and device, as the reference's
+// gemm_choose (api.cu:465-552): every valid (tile, split) is timed on the real operands into a
+// scratch output; the three fastest are re-timed and the best kept. Skipped under stream capture
+// and with HIPINFER_GEMM_AUTOTUNE=0 (the model above decides then).
+std::mutex g_tune_mu;
+std::map<std::tuple<int, int, int, int, bool, bool>, Choice> g_tuned;
+
+int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out) {
+  const HiDevice* d = hi_device();
+  if (!d) return -2;
+  int mb = 16;
+  while (mb < g.M && mb < 4096) mb *= 2;
+  const auto key = std::make_tuple(d->id, mb, g.N, g.K, epi == 2, q8);
+  {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    auto it = g_tuned.find(key);
+    if (it != g_tuned.end()) {
+      *out = it->second;
+      return 0;
+    }
+  }
+  *out = gemm_pick(g.M, g.N, g.K, q8, d->cus);
+  static const bool enabled = !getenv("HIPINFER_GEMM_AUTOTUNE") || atoi(getenv("HIPINFER_GEMM_AUTOTUNE")) != 0;
+  static const bool verbose = getenv("HIPINFER_GEMM_VERBOSE") && atoi(getenv("HIPINFER_GEMM_VERBOSE")) != 0;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HI_TRY(hipStreamIsCapturing(s, &cap));
+  if (!enabled || cap != hipStreamCaptureStatusNone) return 0;
+
+  const int n_out = epi == 2 ? g.N / 2 : g.N;
+  f16* scratch = nullptr;
+  HI_TRY(hipMalloc(&scratch, (size_t)g.M * n_out * sizeof(f16)));
+  HI_TRY(hipMemsetAsync(scratch, 0, (size_t)g.M * n_out * sizeof(f16), s));
+  hipEvent_t e0, e1;
+  HI_TRY(hipEventCreate(&e0));
+  HI_TRY(hipEventCreate(&e1));
+  GemmArgs t = g;
+  t.C = scratch;
+  t.ldc = n_out;
+  auto time_it = [&](Choice c, int reps, float* us) -> int {
+    for (int r = 0; r < 1; r++)
+      if (int rc = launch_choice(t, c, epi, q8, s)) return rc;
+    HI_TRY(hipEventRecord(e0, s));
+    for (int r = 0; r < reps; r++)
+      if (int rc = launch_choice(t, c, epi, q8, s)) return rc;
+    HI_TRY(hipEventRecord(e1, s));
+    HI_TRY(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HI_TRY(hipEventElapsedTime(&ms, e0, e1));
+    *us = ms * 1e3f / reps;
+    return 0;
+  };
+  const int nkt = (g.K + kGemmBK - 1) / kGemmBK;
+  std::vector<std::pair<float, Choice>> timed;
+  int rc = 0;
+  for (int c = 0; c < kGemmNumCfgs && !rc; c++) {
+    const int bm = kGemmCfgs[c].bm, bn = kGemmCfgs[c].bn;
+    const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+    if (bm > 2 * mb && c != 5) continue;  // a tile far taller than M only stages padding
+    for (int sp = 1; sp <= 8 && !rc; sp *= 2) {
+      if (sp > nkt || (sp > 1 && tiles * sp > 4L * d->cus) || tiles > kMaxTiles) continue;
+      float us = 0.f;
+      rc = time_it({c, sp}, 3, &us);
+      if (!rc) timed.push_back({us, {c, sp}});
+    }
+  }
+  if (!rc && !timed.empty()) {
+    const size_t nfin = std::min<size_t>(3, timed.size());
+    std::partial_sort(timed.begin(), timed.begin() + nfin, timed.end(),
+                      [](const auto& a, const auto& b) { return a.first < b.first; });
+    float best = 1e30f;
+    for (size_t f = 0; f < nfin && !rc; f++) {
+      float us = 0.f;
+      rc = time_it(timed[f].second, 5, &us);
+      if (!rc && us < best) {
+        best = us;
+        *out = timed[f].second;
+      }
+    }
+    if (verbose && !rc)
+      fprintf(stderr, "hipinfer_amd gemm autotune M=%d N=%d K=%d epi=%d%s -> cfg %d split %d: %.1f us, %.1f TFLOP/s\n",
+              g.M, g.N, g.K, epi, q8 ? " int8" : "", out->cfg, out->splits, best,
+              2.0 * g.M * g.N * g.K / (best * 1e-6) / 1e12);
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipStreamSynchronize(s);
+  (void)hipFree(scratch);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_tune_mu);
+  g_tuned[key] = *out;
+  return 0;
+}
+
+// Launch with a chosen (tile, split): sets up the split-K workspace (or falls back to one split
+// when it would have to grow inside stream capture).
+int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s) {
+  const HiDevice* d = hi_device();
+  if (!d) return -2;
+  GemmArgs g = g0;
+  const int nkt = (g.K + kGemmBK - 1) / kGemmBK;
+  if (ch.splits > nkt) ch.splits = nkt;
+  int kps = (nkt + ch.splits - 1) / ch.splits;
+  ch.splits = (nkt + kps - 1) / kps;  // no empty splits
+  const int bm = kGemmCfgs[ch.cfg].bm, bn = kGemmCfgs[ch.cfg].bn;
+  const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
+  if (ch.splits > 1) {
+    bool ok = false;
+    if (tiles <= kMaxTiles) {
+      const int r = ensure_ws((size_t)ch.splits * tiles * bm * bn * sizeof(float), s, &ok);
+      if (r) return r;
+    }
+    if (ok) {
+      std::lock_guard<std::mutex> lk(g_ws_mu);
+      g.ws = g_ws[d->id].ws;
+      g.counters = g_ws[d->id].cnt;
+    } else {
+      ch.splits = 1;
+      kps = nkt;
+    }
+  }
+  g.kt_per_split = kps;
+  switch (epi) {
+    case 0: return gemm_run<0>(g, ch.cfg, ch.splits, q8, s);
+    case 1: return gemm_run<1>(g, ch.cfg, ch.splits, q8, s);
+    default: return gemm_run<2>(g, ch.cfg, ch.splits, q8, s);
+  }
+}
+
+
 int gemm_entry(const void* A, int lda, const void* W, const void* scales, const void* bias, void* C, int ldc, int M,
                int N, int K, int epi, void* stream, const char* who) {
   const HiDevice* d = hi_device();
@@ -124,16 +265,6 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
   const bool q8 = scales != nullptr;
   const hipStream_t s = (hipStream_t)stream;
 
-  Choice ch = gemm_pick(M, N, K, q8, d->cus);
-  if (g_force_cfg >= 0 && g_force_cfg < kGemmNumCfgs) ch.cfg = g_force_cfg;
-  if (g_force_splits >= 1) ch.splits = g_force_splits;
-  const int nkt = (K + kGemmBK - 1) / kGemmBK;
-  if (ch.splits > nkt) ch.splits = nkt;
-  const int kps = (nkt + ch.splits - 1) / ch.splits;
-  ch.splits = (nkt + kps - 1) / kps;  // no empty splits
-  const int bm = kGemmCfgs[ch.cfg].bm, bn = kGemmCfgs[ch.cfg].bn;
-  const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-
   GemmArgs g{};
   g.A = (const f16*)A;
   g.lda = lda;
@@ -145,28 +276,15 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
   g.M = M;
   g.N = N;
   g.K = K;
-  g.kt_per_split = kps;
-  if (ch.splits > 1) {
-    bool ok = false;
-    if (tiles > kMaxTiles) ok = false;
-    else {
-      const int r = ensure_ws((size_t)ch.splits * tiles * bm * bn * sizeof(float), s, &ok);
-      if (r) return r;
-    }
-    if (ok) {
-      std::lock_guard<std::mutex> lk(g_ws_mu);
-      g.ws = g_ws[d->id].ws;
-      g.counters = g_ws[d->id].cnt;
-    } else {  // cannot grow under capture: run unsplit
-      ch.splits = 1;
-      g.kt_per_split = nkt;
-    }
+  Choice ch{1, 1};
+  if (g_force_cfg >= 0 && g_force_cfg < kGemmNumCfgs) {
+    ch = gemm_pick(M, N, K, q8, d->cus);
+    ch.cfg = g_force_cfg;
+  } else if (int r = gemm_choose(g, epi, q8, s, &ch)) {
+    return r;
   }
-  switch (epi) {
-    case 0: return gemm_run<0>(g, ch.cfg, ch.splits, q8, s);
-    case 1: return gemm_run<1>(g, ch.cfg, ch.splits, q8, s);
-    default: return gemm_run<2>(g, ch.cfg, ch.splits, q8, s);
-  }
+  if (g_force_splits >= 1) ch.splits = g_force_splits;
+  return launch_choice(g, ch, epi, q8, s);
 }
 
 }  // namespace

@@ -59,7 +59,7 @@ SHAPES = [(128, 2560, 2048), (77, 2048, 5632), (512, 32000, 2048), (1000, 2048, 
           (64, 6144, 4096), (257, 4096, 14336)]
 
 
-@pytest.mark.parametrize("cfg", [-1, 0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("cfg", [-1, 0, 1, 2, 3, 4, 5, 6])
 def test_gemm_configs(hi, O, cfg):
     r = rng(300 + cfg)
     hi.lib.hi_gemm_force_config(cfg)
@@ -128,7 +128,7 @@ def test_gemm_short_k(hi, O):
     tiles leaves no empty split."""
     r = rng(330)
     try:
-        for cfg in [-1, 0, 1, 5]:
+        for cfg in [-1, 0, 1, 5, 6]:
             hi.lib.hi_gemm_force_config(cfg)
             for sp in [1, 2]:
                 hi.lib.hi_gemm_force_splits(sp)
@@ -141,7 +141,7 @@ def test_gemm_short_k(hi, O):
         hi.lib.hi_gemm_force_splits(-1)
 
 
-@pytest.mark.parametrize("cfg", [-1, 0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("cfg", [-1, 0, 1, 2, 3, 4, 5, 6])
 def test_gemm_int8(hi, O, cfg):
     r = rng(340 + cfg)
     H, I = 2048, 5632
