@@ -42,6 +42,13 @@ struct GemmArgs {
   int kt_per_split;    // K tiles per split (gridDim.y splits)
   float* ws;           // split-K partials: [splits][tiles][BM * BN] fp32
   int* counters;       // [tiles] arrival counters, zero between launches
+  // grouped mode (MoE experts): group e owns A/C rows [grp_off[e], grp_off[e+1]) and the weights
+  // at W + e * grp_wstride bytes; its row tiles are [grp_tiles[e], grp_tiles[e+1]) of the global
+  // row-tile count (block id / column tiles)
+  const int* grp_off;
+  const int* grp_tiles;
+  int grp_n;
+  int64_t grp_wstride;
 };
 
 constexpr int kGemmBK = 64;
@@ -67,7 +74,7 @@ __device__ __forceinline__ int lds_off(int r, int c) { return r * kGemmBK + ((c 
 // Byte offset of 16-byte chunk `c` of row `r` in an LDS tile of 64-byte int8 rows.
 __device__ __forceinline__ int lds_off8(int r, int c) { return r * 64 + ((c ^ (r & 3)) << 4); }
 
-template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8>
+template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, bool GRP = false>
 __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
   constexpr int TM = BM / WM, TN = BN / WN;          // wave tile
   constexpr int FM = TM / 32, FN = TN / 32;          // MFMA tiles per wave
@@ -79,24 +86,47 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
   constexpr int L = A_LD + B_LD;                     // vector-memory ops per lane per K tile
   static_assert(WM * WN == 4 && FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tiling");
   static_assert(A_LD >= 1 && B_LD >= 1 && (S - 2) * L < 64 && S >= 2 && S <= 4, "pipeline shape");
+  static_assert(!(GRP && Q8), "grouped (expert) GEMMs take fp16 weights");
   extern __shared__ f16 smem[];
   f16* As = smem;               // [S][BM][64]
   f16* Bs = smem + S * A_ST;    // [S][BN][64] fp16, or [S][BN][64 bytes] int8
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const int M = g.M, N = g.N, K = g.K;
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, ntiles = tiles_m * tiles_n;
-
-  // tile index: blocks are dealt round-robin over the 8 XCDs; give each XCD a contiguous run of
-  // tile ids (the part of the grid that divides by 8; the remainder keeps its id)
-  int pid = blockIdx.x;
-  {
+  const int N = g.N, K = g.K;
+  int M = g.M;
+  const f16* Ap = g.A;
+  f16* Cp = g.C;
+  const char* Wb = reinterpret_cast<const char*>(g.W);
+  const int tiles_n = (N + BN - 1) / BN;
+  int tm, tn, ntiles;
+  if constexpr (GRP) {
+    // find this block's group: grp_tiles[e] <= row tile < grp_tiles[e + 1]; blocks past the last
+    // row tile (the grid is sized for the worst case) exit
+    const int mt = blockIdx.x / tiles_n;
+    tn = blockIdx.x - mt * tiles_n;
+    if (mt >= g.grp_tiles[g.grp_n]) return;
+    int lo = 0, hi = g.grp_n;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (g.grp_tiles[mid] <= mt) lo = mid;
+      else hi = mid;
+    }
+    const int r0 = g.grp_off[lo];
+    M = g.grp_off[lo + 1] - r0;
+    Ap += r0 * g.lda;
+    Cp += r0 * g.ldc;
+    Wb += lo * g.grp_wstride;
+    tm = mt - g.grp_tiles[lo];
+    ntiles = 0;
+  } else {
+    const int tiles_m = (M + BM - 1) / BM;
+    ntiles = tiles_m * tiles_n;
+    // tile index: blocks are dealt round-robin over the 8 XCDs; give each XCD a contiguous run of
+    // tile ids (the part of the grid that divides by 8; the remainder keeps its id)
+    int pid = blockIdx.x;
     const int per = ntiles / 8;
     if (pid < per * 8) pid = (pid % 8) * per + pid / 8;
-  }
-  int tm, tn;
-  {
     constexpr int GM = 8;
     const int per_group = GM * tiles_n, first = (pid / per_group) * GM;
     const int gsize = min(tiles_m - first, GM), r = pid % per_group;
@@ -111,7 +141,6 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
 
   // ---- DMA of one K tile into stage st. Lane l of an instruction covering 8 (A, W fp16) or
   //      16 (W int8) rows fills LDS slot l: it fetches the chunk the swizzle puts there.
-  const char* Wb = reinterpret_cast<const char*>(g.W);
   auto issue = [&](int kt, int st) {
     const int k0 = kt * kGemmBK;
     f16* as = As + st * A_ST;
@@ -120,7 +149,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
       const int r0 = (wave * A_LD + i) * 8, r = r0 + (lane >> 3), lc = (lane & 7) ^ (lane >> 3);
       const int row = min(bm + r, M - 1);
       const int k = k0 + lc * 8 < K ? k0 + lc * 8 : k0;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g.A + row * g.lda + k),
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(Ap + row * g.lda + k),
                                        (lds_void_t*)(as + r0 * kGemmBK), 16, 0, 0);
     }
     f16* bs = Bs + st * B_ST;
@@ -263,10 +292,10 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
           const float up = __shfl_xor(v, 16, kWave);  // column fr + 16 of the same 32-column group
           if (fr < 16 && row < M && col < N) {
             const int oc = ((bn + wn * TN + j * 32) >> 1) + fr;
-            g.C[row * g.ldc + oc] = silu_mul(v, up);
+            Cp[row * g.ldc + oc] = silu_mul(v, up);
           }
         } else if (row < M && col < N) {
-          f16* dst = g.C + row * g.ldc + col;
+          f16* dst = Cp + row * g.ldc + col;
           if constexpr (EPI == 1) *dst = *dst + (f16)v;
           else *dst = (f16)(g.bias ? v + (float)g.bias[col] : v);
         }

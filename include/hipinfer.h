@@ -17,6 +17,8 @@
 #ifndef HIPINFER_AMD_H
 #define HIPINFER_AMD_H
 
+#include <stddef.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -63,6 +65,22 @@ int hi_gemm_force_config(int cfg);
 int hi_gemm_force_splits(int splits);
 int hi_gemm_num_configs(void);
 int hi_gemm_config_desc(int cfg, char* out, int n);
+
+/* ---- mixture of experts (fp16 experts, E <= 256, k <= 16)
+ * Router + top-k of M normalised rows xn[M, H] under Wr[E, H]: idx[M, k] int, w[M, k] fp32, descending;
+ * flags bit 0 = softmax over the k (else over all E), bit 1 = weights rounded to fp16.
+ * Replaces api.cu:849-857 (hi_moe_router); hipinfer.py:68. */
+int hi_moe_router(const void* xn, int ldx, const void* Wr, int M, int E, int H, int k, int flags, int* idx, float* w,
+                  void* stream);
+/* Bytes of the workspace hi_moe_experts needs. Replaces api.cu:862-865 (hi_moe_work_bytes); hipinfer.py:69. */
+size_t hi_moe_work_bytes(int M, int k, int E, int H, int I);
+/* x[m] += MoE(xn[m]) given the routing: wgu [E][2I, H] (gate/up interleaved per expert), wdown [E][H, I];
+ * scale multiplies the combined output (rounded); path 0 auto (GEMV for M <= HIPINFER_GEMV_MAX, default 4),
+ * 1 GEMV, 2 grouped MFMA GEMMs (device-side expert grouping, no host round trip). H % 32 == 0, I % 32 == 0.
+ * Replaces api.cu:872-911 (hi_moe_experts); hipinfer.py:71. */
+int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const void* wdown, const int* idx, const float* w, int M,
+                   int E, int k, int H, int I, int flags, float scale, void* x, int ldx, int path, void* work,
+                   void* stream);
 
 /* ---- RMSNorm (unfused form of the GEMV prologue; the reference's tests build references with it)
  * y[M, H] = w * fp16(x * rsqrt(mean(x^2) + eps)), rows contiguous. Replaces api.cu:76-79
