@@ -6,27 +6,41 @@
 // Design:
 //  * a block of 4 waves owns a BM x BN output tile; each wave a (BM/WM) x (BN/WN) sub-tile built
 //    from v_mfma_f32_32x32x16_f16 tiles (A and W are both K-contiguous, so each lane's 8-half
-//    fragment is one 16-byte LDS read);
+//    fragment is one 16-byte LDS read). The big tiles give each wave a 128 x 128 (or 128 x 64)
+//    sub-tile, so every 16-byte fragment read feeds four (or two) MFMAs;
 //  * K advances in 64-deep tiles through an S-stage ring in LDS fed by gfx950's direct
-//    global->LDS loads (global_load_lds_dwordx4): no register staging, S-1 tiles in flight while
-//    the MFMAs consume the oldest, one explicit vmcnt wait and one barrier per K tile;
-//  * LDS rows hold 16-byte chunks whose position is XOR-swizzled by the row, so the 32 rows one
-//    fragment read touches spread over the banks; the swizzle is applied on the global side (each
-//    lane fetches the chunk that belongs at its LDS slot), since a DMA lane's LDS slot is fixed;
-//  * int8 weights travel to LDS raw (half the bytes) and are dequantised per fragment: exact
-//    int8 -> fp16 unpack, then one packed fp16 multiply by the row scale = fp16(q * s), the weight
-//    the reference's int8 GEMM computes with (kernels.cuh:86-94, 336-341);
-//  * rows past M or N load a clamped (valid) row whose results are never stored; a K tail of 32
-//    skips the last two 16-deep MFMA steps;
+//    global->LDS loads (global_load_lds_dwordx4): no register staging, the next S-1 tiles in flight
+//    while the MFMAs consume the current one;
+//  * within a tile the fragments of step s+1 are read from LDS while the MFMAs of step s run (the
+//    order is pinned with scheduling-group barriers: MFMA, LDS read, MFMA, ...); the one barrier
+//    per tile sits in the last step, after its fragments are in registers, and is followed at once
+//    by the DMA that refills the stage just freed and by the first fragment reads of the next tile.
+//    The refill is unconditional (past the split's last tile it re-reads the first), so the loop
+//    body has no branch and its DMA waits are compile-time counts;
+//  * LDS rows hold 16-byte chunks at positions XOR-swizzled by the row (c ^ ((r >> 1) & 7) for
+//    128-byte rows, c ^ ((r >> 2) & 3) for 64-byte int8 rows): the 16 lanes one 128-bit read serves
+//    per cycle then cover all 64 banks. The swizzle is applied on the global side (each DMA lane
+//    fetches the chunk that belongs at its fixed LDS slot);
+//  * the k order inside each 32-deep half tile is permuted identically for A and W: step 2j + h
+//    gives lane (row, half fk) the k values 32j + 16 fk + 8 h + 0..7. An int8 lane then reads its
+//    two steps' 16 weights as one 16-byte chunk (a conflict-free 128-bit read) and dequantises
+//    them per fragment: exact int8 -> fp16 unpack, one packed fp16 multiply by the row scale =
+//    fp16(q * s), the weight the reference's int8 GEMM computes with (kernels.cuh:86-94, 336-341);
+//  * the DMA goes through buffer resources based at the block's first rows, so each lane keeps
+//    32-bit offsets only and rows past M or N read zeros (never stored); a K tail of 32
+//    (K % 64 == 32) is the last tile's first half only, handled outside the main loop;
 //  * the tile index is remapped so each of the 8 XCDs (blocks are dealt round-robin across them)
 //    gets a contiguous run of tiles, rasterised in groups of 8 tile rows, so the A and W panels a
 //    run needs stay in that XCD's L2;
+//  * the W fragment is the MFMA's first operand, so each lane ends with 16 results of ONE output
+//    row, four consecutive columns per register quad: the epilogue stores 8 bytes at a time, and
+//    a gate column and its up column (16 apart) sit in the same lane -- no cross-lane traffic;
 //  * epilogues (reference kernels.cuh:454-505): 0 store (+ bias, fp32 before the rounding),
-//    1 residual (fp16 add), 2 SwiGLU over 16-column gate/up groups (the partner column sits 16
-//    lanes away in the MFMA result and is fetched with one lane swizzle);
-//  * split-K: gridDim.y blocks share a tile; each writes its fp32 partial to a workspace, and the
-//    last to arrive (device-scope counter, reset for the next launch or graph replay) sums the
-//    partials in split order -- deterministic whatever the arrival order -- and runs the epilogue.
+//    1 residual (fp16 add), 2 SwiGLU over 16-column gate/up groups;
+//  * split-K: gridDim.y blocks share a tile and write fp32 partials [split][M][N]; a second kernel
+//    sums them in split order (deterministic) and runs the epilogue. The kernel boundary makes the
+//    partials visible across XCDs; an in-kernel "last block reduces" handoff would need an
+//    agent-scope fence, which writes back and invalidates the XCD's L2 on this part.
 #pragma once
 #include "hi_common.h"
 
@@ -40,8 +54,8 @@ struct GemmArgs {
   int64_t ldc;
   int M, N, K;
   int kt_per_split;    // K tiles per split (gridDim.y splits)
-  float* ws;           // split-K partials: [splits][tiles][BM * BN] fp32
-  int* counters;       // [tiles] arrival counters, zero between launches
+  float* ws;           // split-K partials: [splits][M][N] fp32
+  bool vec_c;          // C (and the residual read) allow 8-byte accesses: C 8-byte aligned, ldc % 4 == 0
   // grouped mode (MoE experts): group e owns A/C rows [grp_off[e], grp_off[e+1]) and the weights
   // at W + e * grp_wstride bytes; its row tiles are [grp_tiles[e], grp_tiles[e+1]) of the global
   // row-tile count (block id / column tiles)
@@ -61,6 +75,8 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
+// Wait until every LDS read of this wave has returned.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 // Workgroup barrier without a memory fence (a fence would drain every in-flight LDS DMA); the
 // DMA completions it orders are waited for explicitly with wait_vmcnt.
 __device__ __forceinline__ void barrier_no_fence() {
@@ -69,10 +85,41 @@ __device__ __forceinline__ void barrier_no_fence() {
   asm volatile("" ::: "memory");
 }
 
-// Half offset of 16-byte chunk `c` of row `r` in an LDS tile of 64-half (128-byte) rows.
-__device__ __forceinline__ int lds_off(int r, int c) { return r * kGemmBK + ((c ^ (r & 7)) << 3); }
-// Byte offset of 16-byte chunk `c` of row `r` in an LDS tile of 64-byte int8 rows.
-__device__ __forceinline__ int lds_off8(int r, int c) { return r * 64 + ((c ^ (r & 3)) << 4); }
+// Four consecutive fp16 values at p: one 8-byte access when `vec` (p 8-byte aligned), else four.
+__device__ __forceinline__ f16x4 load4(const f16* p, bool vec) {
+  if (vec) return *reinterpret_cast<const f16x4*>(p);
+  return f16x4{p[0], p[1], p[2], p[3]};
+}
+__device__ __forceinline__ void store4(f16* p, f16x4 v, bool vec) {
+  if (vec) {
+    *reinterpret_cast<f16x4*>(p) = v;
+  } else {
+    p[0] = v[0];
+    p[1] = v[1];
+    p[2] = v[2];
+    p[3] = v[3];
+  }
+}
+
+// Half offset of logical 16-byte chunk `c` of row `r` in an LDS tile of 64-half (128-byte) rows.
+__device__ __forceinline__ int lds_off(int r, int c) { return r * kGemmBK + ((c ^ ((r >> 1) & 7)) << 3); }
+// Byte offset of logical 16-byte chunk `c` of row `r` in an LDS tile of 64-byte int8 rows.
+__device__ __forceinline__ int lds_off8(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+
+// Scheduling pattern of one step: the step's NM MFMAs alternate with the ND LDS reads of the next
+// step's fragments (then whichever is left over), so the reads are issued early and their latency
+// hides under the matrix work instead of being sunk next to their first use.
+template <int NM, int ND>
+__device__ __forceinline__ void sched_step() {
+  constexpr int P = ND < NM ? ND : NM;
+#pragma unroll
+  for (int i = 0; i < P; i++) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+  }
+  if constexpr (NM > P) __builtin_amdgcn_sched_group_barrier(0x008, NM - P, 0);
+  if constexpr (ND > P) __builtin_amdgcn_sched_group_barrier(0x100, ND - P, 0);
+}
 
 template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, bool GRP = false>
 __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
@@ -85,9 +132,12 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
   constexpr int B_LD = BN * B_ROWB / 4096;           // ... (W)
   constexpr int L = A_LD + B_LD;                     // vector-memory ops per lane per K tile
   static_assert(WM * WN == 4 && FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tiling");
-  static_assert(A_LD >= 1 && B_LD >= 1 && (S - 2) * L < 64 && S >= 2 && S <= 4, "pipeline shape");
+  static_assert(A_LD >= 1 && B_LD >= 1 && S >= 2 && S <= 4 && 3 * L < 64, "pipeline shape");
   static_assert(!(GRP && Q8), "grouped (expert) GEMMs take fp16 weights");
-  extern __shared__ f16 smem[];
+  // The dynamic LDS follows the static (the split-K flag below); a 16-byte element type makes the
+  // compiler start it on a 16-byte boundary, which every 128-bit LDS access and DMA here needs.
+  extern __shared__ u32x4 smem_raw[];
+  f16* smem = reinterpret_cast<f16*>(smem_raw);
   f16* As = smem;               // [S][BM][64]
   f16* Bs = smem + S * A_ST;    // [S][BN][64] fp16, or [S][BN][64 bytes] int8
 
@@ -137,36 +187,51 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
 
   const int nkt = (K + kGemmBK - 1) / kGemmBK;
   const int kt0 = blockIdx.y * g.kt_per_split;
-  const int nloc = min(nkt, kt0 + g.kt_per_split) - kt0;  // K tiles of this split
+  const int nloc = min(nkt, kt0 + g.kt_per_split) - kt0;  // K tiles of this split (>= 1)
+  const bool half_tail = (K & 63) != 0 && kt0 + nloc == nkt;  // the last tile holds only 32 k
 
-  // ---- DMA of one K tile into stage st. Lane l of an instruction covering 8 (A, W fp16) or
-  //      16 (W int8) rows fills LDS slot l: it fetches the chunk the swizzle puts there.
+  // ---- DMA of one K tile into stage st, through buffer resources based at the block's first A
+  //      and W rows. Lane l of an instruction covering 8 (A, W fp16) or 16 (W int8) rows fills LDS
+  //      slot l: it fetches the chunk the swizzle puts there. Offsets are bounds-checked against
+  //      the rows that exist: rows past M or N read zeros (never stored). Chunks past K (the second
+  //      half of a half tile) read bytes of the next row or zeros, and are never used.
+  const int valid_m = min(M - bm, BM), valid_n = min(N - bn, BN);
+  const __amdgpu_buffer_rsrc_t a_rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<f16*>(Ap + (int64_t)bm * g.lda), (short)0, (int)(((int64_t)(valid_m - 1) * g.lda + K) * 2),
+      0x00020000);
+  const __amdgpu_buffer_rsrc_t b_rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(Wb + (int64_t)bn * K * (Q8 ? 1 : 2)), (short)0, (int)((int64_t)valid_n * K * (Q8 ? 1 : 2)),
+      0x00020000);
+  // this lane's byte offset within an instruction's rows; the swizzle term of a 128-byte row r is
+  // ((r >> 1) & 7), which over an instruction's 8 rows depends on the instruction's parity and
+  // lane / 16; for 64-byte int8 rows, ((r >> 2) & 3) depends on lane / 16 only
+  const int a_r = lane >> 3, a_p = lane & 7;
+  int a_lo[2], b_lo[2];
+#pragma unroll
+  for (int par = 0; par < 2; par++) {
+    const int sw = (par * 4 + (a_r >> 1)) & 7;
+    a_lo[par] = (int)((int64_t)a_r * g.lda * 2) + ((a_p ^ sw) << 4);
+    b_lo[par] = Q8 ? (lane >> 2) * K + (((lane & 3) ^ ((lane >> 4) & 3)) << 4) : a_r * K * 2 + ((a_p ^ sw) << 4);
+  }
   auto issue = [&](int kt, int st) {
     const int k0 = kt * kGemmBK;
     f16* as = As + st * A_ST;
 #pragma unroll
     for (int i = 0; i < A_LD; i++) {
-      const int r0 = (wave * A_LD + i) * 8, r = r0 + (lane >> 3), lc = (lane & 7) ^ (lane >> 3);
-      const int row = min(bm + r, M - 1);
-      const int k = k0 + lc * 8 < K ? k0 + lc * 8 : k0;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(Ap + row * g.lda + k),
-                                       (lds_void_t*)(as + r0 * kGemmBK), 16, 0, 0);
+      const int ri = (wave * A_LD + i) * 8;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_void_t*)(as + ri * kGemmBK), 16,
+                                               a_lo[ri >> 3 & 1] + (int)((int64_t)ri * g.lda * 2) + k0 * 2, 0, 0, 0);
     }
-    f16* bs = Bs + st * B_ST;
+    char* bs = reinterpret_cast<char*>(Bs + st * B_ST);
 #pragma unroll
     for (int i = 0; i < B_LD; i++) {
       if constexpr (Q8) {
-        const int r0 = (wave * B_LD + i) * 16, r = r0 + (lane >> 2), lc = (lane & 3) ^ (r & 3);
-        const int row = min(bn + r, N - 1);
-        const int k = k0 + lc * 16 < K ? k0 + lc * 16 : k0;
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(Wb + (int64_t)row * K + k),
-                                         (lds_void_t*)(reinterpret_cast<char*>(bs) + r0 * 64), 16, 0, 0);
+        const int ri = (wave * B_LD + i) * 16;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rs, (lds_void_t*)(bs + ri * 64), 16, b_lo[0] + ri * K + k0, 0, 0, 0);
       } else {
-        const int r0 = (wave * B_LD + i) * 8, r = r0 + (lane >> 3), lc = (lane & 7) ^ (lane >> 3);
-        const int row = min(bn + r, N - 1);
-        const int k = k0 + lc * 8 < K ? k0 + lc * 8 : k0;
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(Wb + ((int64_t)row * K + k) * 2),
-                                         (lds_void_t*)(bs + r0 * kGemmBK), 16, 0, 0);
+        const int ri = (wave * B_LD + i) * 8;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rs, (lds_void_t*)(bs + ri * 128), 16,
+                                                 b_lo[ri >> 3 & 1] + ri * K * 2 + k0 * 2, 0, 0, 0);
       }
     }
   };
@@ -181,6 +246,35 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
       bsc[j] = f16x2{sv, sv};
     }
   }
+  // LDS offsets of this lane's fragment rows (halves for A / fp16 W, bytes for int8 W), per chunk
+  // parity: the swizzle term of row r is ((r >> 1) & 7) (or (r >> 2) & 3), fixed per lane
+  int a_row[FM], b_row[FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++) a_row[i] = (wm * TM + i * 32 + fr);
+#pragma unroll
+  for (int j = 0; j < FN; j++) b_row[j] = (wn * TN + j * 32 + fr);
+
+  // fragments of step s = 2 jh + h of the tile in stage st
+  auto load_a = [&](int st, int s, f16x8 (&af)[FM]) {
+    const int c = 4 * (s >> 1) + 2 * fk + (s & 1);
+    const f16* as = As + st * A_ST;
+#pragma unroll
+    for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const f16x8*>(as + lds_off(a_row[i], c));
+  };
+  // fp16 W: one fragment per step
+  auto load_b = [&](int st, int s, f16x8 (&bf)[FN]) {
+    const int c = 4 * (s >> 1) + 2 * fk + (s & 1);
+    const f16* bs = Bs + st * B_ST;
+#pragma unroll
+    for (int j = 0; j < FN; j++) bf[j] = *reinterpret_cast<const f16x8*>(bs + lds_off(b_row[j], c));
+  };
+  // int8 W: both steps of half jh as one raw 16-byte chunk
+  auto load_q = [&](int st, int jh, u32x4 (&bq)[FN]) {
+    const char* bs = reinterpret_cast<const char*>(Bs + st * B_ST);
+    const int c = 2 * jh + fk;
+#pragma unroll
+    for (int j = 0; j < FN; j++) bq[j] = *reinterpret_cast<const u32x4*>(bs + lds_off8(b_row[j], c));
+  };
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -190,126 +284,206 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-#pragma unroll
-  for (int s = 0; s < S - 1; s++)
-    if (s < nloc) issue(kt0 + s, s);
-
-  for (int t = 0; t < nloc; t++) {
-    // tile t has landed once at most `later` tiles' DMA remain outstanding
-    const int later = min(S - 2, nloc - 1 - t);
-    if (later >= 2) wait_vmcnt<2 * L>();
-    else if (later == 1) wait_vmcnt<L>();
-    else wait_vmcnt<0>();
-    barrier_no_fence();  // every lane's part of tile t is in LDS; every wave is done with tile t-1
-    if (t + S - 1 < nloc) issue(kt0 + t + S - 1, (t + S - 1) % S);
-
-    const int st = t % S, k0 = (kt0 + t) * kGemmBK;
-    const f16* as = As + st * A_ST;
-    const f16* bs = Bs + st * B_ST;
-#pragma unroll
-    for (int ks = 0; ks < kGemmBK / 16; ks++) {
-      if (k0 + ks * 16 < K) {
-        const int ch = ks * 2 + fk;
-        f16x8 af[FM], bf[FN];
-#pragma unroll
-        for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const f16x8*>(as + lds_off(wm * TM + i * 32 + fr, ch));
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-          if constexpr (Q8) {
-            const int r = wn * TN + j * 32 + fr;
-            const u32x2 q = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(bs) + lds_off8(r, ks) + 8 * fk);
-            f16x2 p0, p1, p2, p3;
-            i8x4_to_f16(q[0], p0, p1);
-            i8x4_to_f16(q[1], p2, p3);
-            p0 = p0 * bsc[j];  // fp16(q * s), one rounding each
-            p1 = p1 * bsc[j];
-            p2 = p2 * bsc[j];
-            p3 = p3 * bsc[j];
-            bf[j] = f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-          } else {
-            bf[j] = *reinterpret_cast<const f16x8*>(bs + lds_off(wn * TN + j * 32 + fr, ch));
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-          for (int j = 0; j < FN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-      }
-    }
-  }
-
-  // ---- split-K: partial to the workspace; the last block of the tile reduces in split order
-  const int splits = gridDim.y;
-  const int tile = tm * tiles_n + tn;
-  if (splits > 1) {
-    float* part = g.ws + ((int64_t)blockIdx.y * ntiles + tile) * (BM * BN);
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int j = 0; j < FN; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int r = wm * TM + i * 32 + 8 * (e >> 2) + 4 * fk + (e & 3), c = wn * TN + j * 32 + fr;
-          part[r * BN + c] = acc[i][j][e];
-        }
-    __threadfence();
-    __syncthreads();
-    __shared__ int last;
-    if (tid == 0) {
-      const int prev = atomicAdd(&g.counters[tile], 1);
-      last = prev == splits - 1;
-      if (last) g.counters[tile] = 0;  // ready for the next launch / graph replay
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int j = 0; j < FN; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int r = wm * TM + i * 32 + 8 * (e >> 2) + 4 * fk + (e & 3), c = wn * TN + j * 32 + fr;
-          float t = 0.f;
-          for (int z = 0; z < splits; z++)
-            t += __builtin_nontemporal_load(g.ws + ((int64_t)z * ntiles + tile) * (BM * BN) + r * BN + c);
-          acc[i][j][e] = t;
-        }
-  }
-
-  // ---- epilogue straight from the MFMA result layout: lane (fk, fr) of tile (i, j) holds rows
-  //      8*(e/4) + 4*fk + e%4 of column fr
-#pragma unroll
-  for (int i = 0; i < FM; i++)
+  // the MFMAs of one step; int8 fragments are dequantised from half h of the raw chunk
+  auto mfmas = [&](int h, const f16x8 (&af)[FM], const f16x8 (&bf)[FN], const u32x4 (&bq)[FN]) {
+    f16x8 b[FN];
 #pragma unroll
     for (int j = 0; j < FN; j++) {
-      const int col = bn + wn * TN + j * 32 + fr;
+      if constexpr (Q8) {
+        f16x2 p0, p1, p2, p3;
+        i8x4_to_f16(bq[j][2 * h], p0, p1);
+        i8x4_to_f16(bq[j][2 * h + 1], p2, p3);
+        p0 = p0 * bsc[j];  // fp16(q * s), one rounding each
+        p1 = p1 * bsc[j];
+        p2 = p2 * bsc[j];
+        p3 = p3 * bsc[j];
+        b[j] = f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+      } else {
+        b[j] = bf[j];
+      }
+    }
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int row = bm + wm * TM + i * 32 + 8 * (e >> 2) + 4 * fk + (e & 3);
-        const float v = acc[i][j][e];
-        if constexpr (EPI == 2) {
-          const float up = __shfl_xor(v, 16, kWave);  // column fr + 16 of the same 32-column group
-          if (fr < 16 && row < M && col < N) {
-            const int oc = ((bn + wn * TN + j * 32) >> 1) + fr;
-            Cp[row * g.ldc + oc] = silu_mul(v, up);
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[j], af[i], acc[i][j], 0, 0, 0);
+  };
+
+  // ---- prologue: S tiles in flight (past the split's last tile, its first tile again: a stage is
+  //      filled every time, so the outstanding-DMA count is the same in every iteration), the
+  //      first fragments of tile 0 in registers
+  auto tile_or_first = [&](int kt) { return kt < kt0 + nloc ? kt : kt0; };
+#pragma unroll
+  for (int s = 0; s < S; s++) issue(tile_or_first(kt0 + s), s);
+  wait_vmcnt<(S - 1) * L>();
+  barrier_no_fence();
+  f16x8 af0[FM], af1[FM], bf0[FN], bf1[FN];
+  u32x4 bq0[FN], bq1[FN];  // int8: raw chunks of the tile's first and second 32-deep half
+  load_a(0, 0, af0);
+  if constexpr (Q8) load_q(0, 0, bq0);
+  else load_b(0, 0, bf0);
+
+  constexpr int NM = FM * FN;               // MFMAs per step
+  constexpr int ND = FM + (Q8 ? 0 : FN);    // LDS reads per step (int8 W: + FN every other step)
+  // ---- main loop over all tiles but the last: 4 steps each, fragments one step ahead
+  for (int t = 0; t < nloc - 1; t++) {
+    const int st = t % S;
+    load_a(st, 1, af1);
+    if constexpr (!Q8) load_b(st, 1, bf1);
+    mfmas(0, af0, bf0, bq0);
+    sched_step<NM, ND>();
+    load_a(st, 2, af0);
+    if constexpr (Q8) load_q(st, 1, bq1);
+    else load_b(st, 2, bf0);
+    mfmas(1, af1, bf1, bq0);
+    sched_step<NM, ND + (Q8 ? FN : 0)>();
+    load_a(st, 3, af1);
+    if constexpr (!Q8) load_b(st, 3, bf1);
+    mfmas(0, af0, bf0, bq1);
+    sched_step<NM, ND>();
+    // the tile's last fragments are in registers: free its stage, refill it, start the next tile
+    wait_lgkm0();
+    wait_vmcnt<(S - 2) * L>();
+    barrier_no_fence();
+    issue(tile_or_first(kt0 + t + S), st);
+    const int sn = (t + 1) % S;
+    load_a(sn, 0, af0);
+    if constexpr (Q8) load_q(sn, 0, bq0);
+    else load_b(sn, 0, bf0);
+    mfmas(1, af1, bf1, bq1);
+    sched_step<NM, ND + (Q8 ? FN : 0)>();
+  }
+  // ---- the last tile (its first half only when K % 64 == 32)
+  {
+    const int st = (nloc - 1) % S;
+    load_a(st, 1, af1);
+    if constexpr (!Q8) load_b(st, 1, bf1);
+    mfmas(0, af0, bf0, bq0);
+    mfmas(1, af1, bf1, bq0);
+    if (!half_tail) {
+      load_a(st, 2, af0);
+      load_a(st, 3, af1);
+      if constexpr (Q8) {
+        load_q(st, 1, bq1);
+      } else {
+        load_b(st, 2, bf0);
+        load_b(st, 3, bf1);
+      }
+      mfmas(0, af0, bf0, bq1);
+      mfmas(1, af1, bf1, bq1);
+    }
+  }
+  wait_vmcnt<0>();  // the refills issued past the last tile have landed before the block ends
+
+  // ---- result layout (W fragment as the MFMA's first operand): lane (fk, fr) of tile (i, j) holds
+  //      row fr of the tile's 32 rows, columns 8 g + 4 fk + 0..3 in acc[i][j][4 g .. 4 g + 3]:
+  //      four consecutive output columns per register quad
+  if (gridDim.y > 1) {
+    // split-K: this split's fp32 partial [split][M][N]; a second kernel (gemm_splitk_reduce) sums
+    // the splits in order and runs the epilogue, after the kernel boundary made them visible
+    float* part = g.ws + (int64_t)blockIdx.y * M * N;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      const int row = bm + wm * TM + i * 32 + fr;
+      if (row >= M) continue;
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int col = bn + wn * TN + j * 32 + 8 * q + 4 * fk;
+          if (col < N)
+            *reinterpret_cast<f32x4*>(part + (int64_t)row * N + col) =
+                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; i++) {
+    const int row = bm + wm * TM + i * 32 + fr;
+    if (row >= M) continue;
+    f16* crow = Cp + (int64_t)row * g.ldc;
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int c0 = bn + wn * TN + j * 32;  // first column of the 32-column MFMA tile
+      if (c0 >= N) continue;
+      if constexpr (EPI == 2) {
+        // gate columns c0 + 0..15 and their up columns c0 + 16..31 sit in the same lane
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+          f16x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; e++) o[e] = silu_mul_fast(acc[i][j][4 * q + e], acc[i][j][4 * q + 8 + e]);
+          store4(crow + (c0 >> 1) + 8 * q + 4 * fk, o, g.vec_c);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int col = c0 + 8 * q + 4 * fk;
+          f16x4 o;
+          if constexpr (EPI == 1) {
+            const f16x4 r = load4(crow + col, g.vec_c);
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = r[e] + (f16)acc[i][j][4 * q + e];  // fp16 add, rounded
+          } else {
+            f16x4 b = {(f16)0.f, (f16)0.f, (f16)0.f, (f16)0.f};
+            if (g.bias) b = load4(g.bias + col, ((uintptr_t)g.bias & 7) == 0);
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = (f16)(acc[i][j][4 * q + e] + (float)b[e]);
           }
-        } else if (row < M && col < N) {
-          f16* dst = Cp + row * g.ldc + col;
-          if constexpr (EPI == 1) *dst = *dst + (f16)v;
-          else *dst = (f16)(g.bias ? v + (float)g.bias[col] : v);
+          store4(crow + col, o, g.vec_c);
         }
       }
     }
+  }
+}
+
+// Split-K second pass: sum the fp32 partials [splits][M][N] in split order (deterministic) and run
+// the epilogue with the main kernel's rounding; each thread owns 4 consecutive output columns.
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_splitk_reduce(const float* __restrict__ ws, int splits, int M, int N,
+                                                          const f16* __restrict__ bias, f16* C, int64_t ldc,
+                                                          bool vec_c) {
+  const int n_out = EPI == 2 ? N / 2 : N;
+  const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (idx >= (int64_t)M * n_out) return;
+  const int row = (int)(idx / n_out), oc = (int)(idx - (int64_t)row * n_out);
+  const int64_t plane = (int64_t)M * N;
+  f16* dst = C + (int64_t)row * ldc + oc;
+  f16x4 o;
+  if constexpr (EPI == 2) {
+    const int gc = (oc >> 4) * 32 + (oc & 15);  // gate column; its up column is gc + 16
+    f32x4 gs = {0.f, 0.f, 0.f, 0.f}, us = gs;
+    for (int z = 0; z < splits; z++) {
+      gs += *reinterpret_cast<const f32x4*>(ws + z * plane + (int64_t)row * N + gc);
+      us += *reinterpret_cast<const f32x4*>(ws + z * plane + (int64_t)row * N + gc + 16);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = silu_mul_fast(gs[e], us[e]);
+  } else {
+    f32x4 t = {0.f, 0.f, 0.f, 0.f};
+    for (int z = 0; z < splits; z++) t += *reinterpret_cast<const f32x4*>(ws + z * plane + (int64_t)row * N + oc);
+    if constexpr (EPI == 1) {
+      const f16x4 r = load4(dst, vec_c);
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = r[e] + (f16)t[e];
+    } else {
+      f16x4 b = {(f16)0.f, (f16)0.f, (f16)0.f, (f16)0.f};
+      if (bias) b = load4(bias + oc, ((uintptr_t)bias & 7) == 0);
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = (f16)(t[e] + (float)b[e]);
+    }
+  }
+  store4(dst, o, vec_c);
 }
 
 // Tile configurations (all 4 waves, BK = 64): {BM, BN, WM, WN, stages}.
 struct GemmCfg {
   int bm, bn, wm, wn, st;
 };
-constexpr GemmCfg kGemmCfgs[] = {{256, 128, 2, 2, 3}, {128, 128, 2, 2, 4}, {128, 64, 2, 2, 4}, {64, 128, 2, 2, 4},
-                                 {64, 64, 2, 2, 4},   {32, 128, 1, 4, 4},  {256, 256, 2, 2, 2}};
+constexpr GemmCfg kGemmCfgs[] = {{256, 256, 2, 2, 2}, {256, 128, 2, 2, 3}, {128, 256, 2, 2, 3}, {64, 128, 2, 2, 4},
+                                 {128, 128, 2, 2, 2}, {64, 64, 2, 2, 4},   {32, 128, 1, 4, 4}, {128, 64, 2, 2, 4}};
 constexpr int kGemmNumCfgs = sizeof(kGemmCfgs) / sizeof(kGemmCfgs[0]);
+constexpr int kGemmGrpCfg = 3;  // the grouped (MoE expert) GEMM's tile: 64 x 128
 inline size_t gemm_lds_bytes(int cfg, bool q8) {
   const GemmCfg& c = kGemmCfgs[cfg];
   return (size_t)c.st * (c.bm * kGemmBK * 2 + c.bn * (q8 ? 64 : 128));
@@ -325,6 +499,12 @@ int gemm_launch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
   const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
   hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, EPI, Q8>), dim3(tiles, splits), dim3(kGemmThreads), lds, s, g);
   HI_TRY(hipGetLastError());
+  if (splits > 1) {
+    const int64_t quads = (int64_t)g.M * (EPI == 2 ? g.N / 2 : g.N) / 4;
+    hipLaunchKernelGGL(gemm_splitk_reduce<EPI>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, g.ws, splits,
+                       g.M, g.N, g.bias, g.C, g.ldc, g.vec_c);
+    HI_TRY(hipGetLastError());
+  }
   return 0;
 }
 
@@ -350,14 +530,15 @@ int gemm_blocks_per_cu(int cfg, bool q8);
   int gemm_run<EPIV>(const GemmArgs& g, int cfg, int splits, bool q8, hipStream_t s) {                        \
     constexpr int EPI = EPIV;                                                                                  \
     HI_GEMM_CFG(0, false) HI_GEMM_CFG(1, false) HI_GEMM_CFG(2, false) HI_GEMM_CFG(3, false)                    \
-    HI_GEMM_CFG(4, false) HI_GEMM_CFG(5, false) HI_GEMM_CFG(6, false)                                          \
+    HI_GEMM_CFG(4, false) HI_GEMM_CFG(5, false) HI_GEMM_CFG(6, false) HI_GEMM_CFG(7, false)                    \
     HI_GEMM_CFG(0, true) HI_GEMM_CFG(1, true) HI_GEMM_CFG(2, true) HI_GEMM_CFG(3, true)                        \
-    HI_GEMM_CFG(4, true) HI_GEMM_CFG(5, true) HI_GEMM_CFG(6, true)                                             \
+    HI_GEMM_CFG(4, true) HI_GEMM_CFG(5, true) HI_GEMM_CFG(6, true) HI_GEMM_CFG(7, true)                        \
     HI_FAIL("gemm: no kernel for config %d", cfg);                                                             \
   }                                                                                                            \
   template <>                                                                                                  \
   int gemm_blocks_per_cu<EPIV>(int cfg, bool q8) {                                                             \
     constexpr int EPI = EPIV;                                                                                  \
     HI_GEMM_OCC(0) HI_GEMM_OCC(1) HI_GEMM_OCC(2) HI_GEMM_OCC(3) HI_GEMM_OCC(4) HI_GEMM_OCC(5) HI_GEMM_OCC(6)    \
+    HI_GEMM_OCC(7)                                                                                             \
     return -1;                                                                                                 \
   }

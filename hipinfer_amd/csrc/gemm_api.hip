@@ -31,7 +31,6 @@ constexpr int kMaxTiles = 1 << 16;
 struct SplitWs {
   float* ws = nullptr;
   size_t bytes = 0;
-  int* cnt = nullptr;
   std::vector<float*> retired;  // outgrown buffers, still referenced by captured graphs
 };
 std::mutex g_ws_mu;
@@ -50,7 +49,7 @@ int cfg_blocks_per_cu(int cfg, bool q8) {
 }
 
 // Relative MFMA efficiency of each tile shape (bigger tiles reuse more of what they stage).
-constexpr double kCfgEff[kGemmNumCfgs] = {1.0, 0.85, 0.7, 0.7, 0.5, 0.45, 1.0};
+constexpr double kCfgEff[kGemmNumCfgs] = {1.0, 0.9, 0.9, 0.6, 0.7, 0.45, 0.4, 0.6};
 
 struct Choice {
   int cfg, splits;
@@ -76,7 +75,7 @@ Choice gemm_pick(int M, int N, int K, bool q8, int cus) {
       const double t_mfma = rounds * 2.0 * bm * bn * kps * kGemmBK / (mfma_per_cu * kCfgEff[c]);
       const double t_l2 = tiles * sp * kps * (double)(bm * 128 + bn * (q8 ? 64 : 128)) / l2_bw;
       double t = std::max(t_mfma, t_l2) + 2e-6;
-      if (sp > 1) t += tiles * sp * bm * bn * 8.0 / 4e12 + 2e-6;
+      if (sp > 1) t += (double)M * N * sp * 8.0 / 4e12 + 3e-6;  // partials out and back, second launch
       if (t < best_t) {
         best_t = t;
         best = {c, sp};
@@ -86,32 +85,26 @@ Choice gemm_pick(int M, int N, int K, bool q8, int cus) {
   return best;
 }
 
-// Workspace for `bytes` of partials (and the tile counters); false when it would have to grow
-// inside stream capture.
+// Workspace for `bytes` of split-K partials; *ok = false when it would have to grow inside stream
+// capture (the caller then runs one split). Every partial is written before it is read, so the
+// buffer needs no clearing.
 int ensure_ws(size_t bytes, hipStream_t s, bool* ok) {
   const HiDevice* d = hi_device();
   if (!d) return -2;
   std::lock_guard<std::mutex> lk(g_ws_mu);
   SplitWs& w = g_ws[d->id];
   *ok = true;
-  if (w.cnt && bytes <= w.bytes) return 0;
+  if (w.ws && bytes <= w.bytes) return 0;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   HI_TRY(hipStreamIsCapturing(s, &cap));
   if (cap != hipStreamCaptureStatusNone) {
     *ok = false;
     return 0;
   }
-  if (!w.cnt) {
-    HI_TRY(hipMalloc(&w.cnt, kMaxTiles * sizeof(int)));
-    HI_TRY(hipMemset(w.cnt, 0, kMaxTiles * sizeof(int)));
-  }
-  if (bytes > w.bytes) {
-    size_t nb = bytes > 2 * w.bytes ? bytes : 2 * w.bytes;
-    if (w.ws) w.retired.push_back(w.ws);
-    HI_TRY(hipMalloc(&w.ws, nb));
-    w.bytes = nb;
-  }
-  HI_TRY(hipDeviceSynchronize());  // the counters' zeroing is complete before any kernel uses them
+  size_t nb = bytes > 2 * w.bytes ? bytes : 2 * w.bytes;
+  if (w.ws) w.retired.push_back(w.ws);
+  HI_TRY(hipMalloc(&w.ws, nb));
+  w.bytes = nb;
   return 0;
 }
 
@@ -176,7 +169,7 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
   for (int c = 0; c < kGemmNumCfgs && !rc; c++) {
     const int bm = kGemmCfgs[c].bm, bn = kGemmCfgs[c].bn;
     const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
-    if (bm > 2 * mb && c != 5) continue;  // a tile far taller than M only stages padding
+    if (bm > 2 * mb && kGemmCfgs[c].bm != 32) continue;  // a tile far taller than M only stages padding
     for (int sp = 1; sp <= 8 && !rc; sp *= 2) {
       if (sp > nkt || (sp > 1 && tiles * sp > 4L * d->cus) || tiles > kMaxTiles) continue;
       float us = 0.f;
@@ -227,13 +220,12 @@ int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s
   if (ch.splits > 1) {
     bool ok = false;
     if (tiles <= kMaxTiles) {
-      const int r = ensure_ws((size_t)ch.splits * tiles * bm * bn * sizeof(float), s, &ok);
+      const int r = ensure_ws((size_t)ch.splits * g.M * g.N * sizeof(float), s, &ok);
       if (r) return r;
     }
     if (ok) {
       std::lock_guard<std::mutex> lk(g_ws_mu);
       g.ws = g_ws[d->id].ws;
-      g.counters = g_ws[d->id].cnt;
     } else {
       ch.splits = 1;
       kps = nkt;
@@ -276,6 +268,7 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
   g.M = M;
   g.N = N;
   g.K = K;
+  g.vec_c = aligned(C, 8) && ldc % 4 == 0;
   Choice ch{1, 1};
   if (g_force_cfg >= 0 && g_force_cfg < kGemmNumCfgs) {
     ch = gemm_pick(M, N, K, q8, d->cus);

@@ -107,6 +107,16 @@ __device__ __forceinline__ f16 silu_mul(float g, float u) {
   return s * (f16)u;  // fp16 product, correctly rounded
 }
 
+// The same rounding points with the division done as gh * rcp(1 + e) (v_rcp_f32, 1 ulp): the
+// fp32 quotient differs from the IEEE one by at most ~1.5 ulp before its rounding to fp16, so the
+// fp16 result matches except when that quotient lies within 1.5 fp32 ulp of an fp16 rounding
+// boundary (then it is one fp16 ulp off). For epilogues that produce thousands of values per lane.
+__device__ __forceinline__ f16 silu_mul_fast(float g, float u) {
+  const float gh = (float)(f16)g;
+  const f16 s = (f16)(gh * __builtin_amdgcn_rcpf(1.0f + __expf(-gh)));
+  return s * (f16)u;
+}
+
 // One RoPE pair with PyTorch's per-op fp16 rounding (reference src/kernels.cuh:132-136).
 __device__ __forceinline__ void rope_pair(f16& y1, f16& y2, f16x2 cs) {
   const float c = (float)cs.x, sn = (float)cs.y, f1 = (float)y1, f2 = (float)y2;

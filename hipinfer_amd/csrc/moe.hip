@@ -28,7 +28,7 @@ namespace {
 
 constexpr int kMoeMaxE = 256, kMoeMaxK = 16;
 constexpr int kMoeNormTopk = 1, kMoeFp16Weights = 2;
-constexpr int kGrpBM = 64, kGrpBN = 128;  // grouped GEMM tile (gemm config 3)
+constexpr int kGrpBM = 64, kGrpBN = 128;  // grouped GEMM tile (gemm config kGemmGrpCfg)
 
 // v beats (best, bi): NaN above numbers; equal values (and NaN vs NaN) go to the lower index
 // (reference argmax_better, kernels.cuh:1886-1890).
@@ -307,7 +307,7 @@ __global__ void __launch_bounds__(128) moe_combine_kernel(const f16* __restrict_
 template <int EPI>
 int grouped_gemm(const f16* A, int lda, const f16* W, int64_t wstride_bytes, f16* C, int ldc, int N, int K,
                  const int* off, const int* tiles, int E, int max_row_tiles, hipStream_t s) {
-  constexpr int cfg = 3;
+  constexpr int cfg = kGemmGrpCfg;
   static_assert(kGemmCfgs[cfg].bm == kGrpBM && kGemmCfgs[cfg].bn == kGrpBN, "grouped tile");
   GemmArgs g{};
   g.A = A;
@@ -319,6 +319,7 @@ int grouped_gemm(const f16* A, int lda, const f16* W, int64_t wstride_bytes, f16
   g.N = N;
   g.K = K;
   g.kt_per_split = (K + kGemmBK - 1) / kGemmBK;
+  g.vec_c = true;  // act / y live in the 256-byte aligned work buffer, ldc = I or H (multiples of 32)
   g.grp_off = off;
   g.grp_tiles = tiles;
   g.grp_n = E;
