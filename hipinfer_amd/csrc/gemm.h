@@ -4,10 +4,11 @@
 // (src/kernels.cuh:305-506) behind the same C-ABI (hi_gemm, hi_gemm_w8; api.cu:566-577).
 //
 // Design:
-//  * a block of 4 waves owns a BM x BN output tile; each wave a (BM/WM) x (BN/WN) sub-tile built
-//    from v_mfma_f32_32x32x16_f16 tiles (A and W are both K-contiguous, so each lane's 8-half
-//    fragment is one 16-byte LDS read). The big tiles give each wave a 128 x 128 (or 128 x 64)
-//    sub-tile, so every 16-byte fragment read feeds four (or two) MFMAs;
+//  * a block of WM x WN waves (4 or 8) owns a BM x BN output tile; each wave a (BM/WM) x (BN/WN)
+//    sub-tile built from v_mfma_f32_32x32x16_f16 tiles (A and W are both K-contiguous, so each
+//    lane's 8-half fragment is one 16-byte LDS read). The big tiles give each wave a 128 x 128 (or
+//    128 x 64) sub-tile, so every 16-byte fragment read feeds four (or two) MFMAs; with 8 waves two
+//    share each SIMD, so one wave's MFMAs cover the other's LDS waits, barrier and DMA issue;
 //  * K advances in 64-deep tiles through an S-stage ring in LDS fed by gfx950's direct
 //    global->LDS loads (global_load_lds_dwordx4): no register staging, the next S-1 tiles in flight
 //    while the MFMAs consume the current one;
@@ -66,7 +67,6 @@ struct GemmArgs {
 };
 
 constexpr int kGemmBK = 64;
-constexpr int kGemmThreads = 256;
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Wait until at most N vector-memory operations (global loads, LDS DMA) are outstanding.
@@ -122,16 +122,17 @@ __device__ __forceinline__ void sched_step() {
 }
 
 template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, bool GRP = false>
-__global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   constexpr int TM = BM / WM, TN = BN / WN;          // wave tile
   constexpr int FM = TM / 32, FN = TN / 32;          // MFMA tiles per wave
   constexpr int A_ST = BM * kGemmBK;                 // halves per stage
   constexpr int B_ROWB = Q8 ? 64 : 128;              // bytes of one W row per K tile
   constexpr int B_ST = BN * B_ROWB / 2;              // halves per stage
-  constexpr int A_LD = BM / 32;                      // 1 KB DMA instructions per wave per K tile (A)
-  constexpr int B_LD = BN * B_ROWB / 4096;           // ... (W)
+  constexpr int NW = WM * WN;                        // waves per block (4 or 8)
+  constexpr int A_LD = BM * 128 / 1024 / NW;         // 1 KB DMA instructions per wave per K tile (A)
+  constexpr int B_LD = BN * B_ROWB / 1024 / NW;      // ... (W)
   constexpr int L = A_LD + B_LD;                     // vector-memory ops per lane per K tile
-  static_assert(WM * WN == 4 && FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tiling");
+  static_assert((NW == 4 || NW == 8) && FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tiling");
   static_assert(A_LD >= 1 && B_LD >= 1 && S >= 2 && S <= 4 && 3 * L < 64, "pipeline shape");
   static_assert(!(GRP && Q8), "grouped (expert) GEMMs take fp16 weights");
   // The dynamic LDS follows the static (the split-K flag below); a 16-byte element type makes the
@@ -476,12 +477,13 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(const float* __restric
   store4(dst, o, vec_c);
 }
 
-// Tile configurations (all 4 waves, BK = 64): {BM, BN, WM, WN, stages}.
+// Tile configurations (BK = 64): {BM, BN, WM, WN, stages}; WM x WN waves per block.
 struct GemmCfg {
   int bm, bn, wm, wn, st;
 };
 constexpr GemmCfg kGemmCfgs[] = {{256, 256, 2, 2, 2}, {256, 128, 2, 2, 3}, {128, 256, 2, 2, 3}, {64, 128, 2, 2, 4},
-                                 {128, 128, 2, 2, 2}, {64, 64, 2, 2, 4},   {32, 128, 1, 4, 4}, {128, 64, 2, 2, 4}};
+                                 {128, 128, 2, 2, 2}, {64, 64, 2, 2, 4},   {32, 128, 1, 4, 4}, {128, 64, 2, 2, 4},
+                                 {256, 256, 2, 4, 2}, {256, 128, 2, 4, 3}};
 constexpr int kGemmNumCfgs = sizeof(kGemmCfgs) / sizeof(kGemmCfgs[0]);
 constexpr int kGemmGrpCfg = 3;  // the grouped (MoE expert) GEMM's tile: 64 x 128
 inline size_t gemm_lds_bytes(int cfg, bool q8) {
@@ -493,11 +495,11 @@ template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8>
 int gemm_launch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
   const size_t lds = gemm_lds_bytes(cfg, Q8);
   const void* fn = reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WM, WN, S, EPI, Q8>);
-  const int bpc = hi_blocks_per_cu(fn, kGemmThreads, lds);  // also lifts the dynamic-LDS limit
+  const int bpc = hi_blocks_per_cu(fn, 64 * WM * WN, lds);  // also lifts the dynamic-LDS limit
   if (bpc < 0) return -2;
   if (bpc == 0) HI_FAIL("gemm: tile %dx%d does not fit on a CU", BM, BN);
   const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, EPI, Q8>), dim3(tiles, splits), dim3(kGemmThreads), lds, s, g);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, EPI, Q8>), dim3(tiles, splits), dim3(64 * WM * WN), lds, s, g);
   HI_TRY(hipGetLastError());
   if (splits > 1) {
     const int64_t quads = (int64_t)g.M * (EPI == 2 ? g.N / 2 : g.N) / 4;
@@ -524,21 +526,23 @@ int gemm_blocks_per_cu(int cfg, bool q8);
   if (cfg == i)                                                                                                \
     return hi_blocks_per_cu(q8 ? reinterpret_cast<const void*>(&HI_GEMM_K(i, true))                            \
                                : reinterpret_cast<const void*>(&HI_GEMM_K(i, false)),                          \
-                            kGemmThreads, gemm_lds_bytes(i, q8));
+                            64 * kGemmCfgs[i].wm * kGemmCfgs[i].wn, gemm_lds_bytes(i, q8));
 #define HI_GEMM_DEFINE_RUN(EPIV)                                                                               \
   template <>                                                                                                  \
   int gemm_run<EPIV>(const GemmArgs& g, int cfg, int splits, bool q8, hipStream_t s) {                        \
     constexpr int EPI = EPIV;                                                                                  \
     HI_GEMM_CFG(0, false) HI_GEMM_CFG(1, false) HI_GEMM_CFG(2, false) HI_GEMM_CFG(3, false)                    \
     HI_GEMM_CFG(4, false) HI_GEMM_CFG(5, false) HI_GEMM_CFG(6, false) HI_GEMM_CFG(7, false)                    \
+    HI_GEMM_CFG(8, false) HI_GEMM_CFG(9, false)                                                                \
     HI_GEMM_CFG(0, true) HI_GEMM_CFG(1, true) HI_GEMM_CFG(2, true) HI_GEMM_CFG(3, true)                        \
     HI_GEMM_CFG(4, true) HI_GEMM_CFG(5, true) HI_GEMM_CFG(6, true) HI_GEMM_CFG(7, true)                        \
+    HI_GEMM_CFG(8, true) HI_GEMM_CFG(9, true)                                                                  \
     HI_FAIL("gemm: no kernel for config %d", cfg);                                                             \
   }                                                                                                            \
   template <>                                                                                                  \
   int gemm_blocks_per_cu<EPIV>(int cfg, bool q8) {                                                             \
     constexpr int EPI = EPIV;                                                                                  \
     HI_GEMM_OCC(0) HI_GEMM_OCC(1) HI_GEMM_OCC(2) HI_GEMM_OCC(3) HI_GEMM_OCC(4) HI_GEMM_OCC(5) HI_GEMM_OCC(6)    \
-    HI_GEMM_OCC(7)                                                                                             \
+    HI_GEMM_OCC(7) HI_GEMM_OCC(8) HI_GEMM_OCC(9)                                                               \
     return -1;                                                                                                 \
   }

@@ -49,7 +49,7 @@ int cfg_blocks_per_cu(int cfg, bool q8) {
 }
 
 // Relative MFMA efficiency of each tile shape (bigger tiles reuse more of what they stage).
-constexpr double kCfgEff[kGemmNumCfgs] = {1.0, 0.9, 0.9, 0.6, 0.7, 0.45, 0.4, 0.6};
+constexpr double kCfgEff[kGemmNumCfgs] = {0.9, 0.85, 0.85, 0.6, 0.8, 0.45, 0.4, 0.6, 1.0, 0.9};
 
 struct Choice {
   int cfg, splits;
@@ -113,8 +113,9 @@ bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0;
 int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s);
 
 // First-call autotuning per (M bucket, N, K, SwiGLU, int8) and device, as the reference's
-// gemm_choose (api.cu:465-552): every valid (tile, split) is timed on the real operands into a
-// scratch output; the three fastest are re-timed and the best kept. Skipped under stream capture
+// gemm_choose (api.cu:465-552): every valid (tile, split) is timed on the real activations into a
+// scratch output, with the weights streamed cold (below); the three fastest are re-timed and the
+// best kept. Skipped under stream capture
 // and with HIPINFER_GEMM_AUTOTUNE=0 (the model above decides then).
 std::mutex g_tune_mu;
 std::map<std::tuple<int, int, int, int, bool, bool>, Choice> g_tuned;
@@ -150,12 +151,27 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
   GemmArgs t = g;
   t.C = scratch;
   t.ldc = n_out;
+  // Candidates are timed on rotating scratch weight buffers (at least ~640 MB in all, so neither
+  // the L2s nor the 256 MB MALL hold them): a prefill streams each layer's weights once, and
+  // timing on the same, cache-resident weights would favour tiles that re-read more. The scratch
+  // contents are never initialised: MFMA timing does not depend on the values, and the results
+  // go to the scratch output.
+  const size_t wstride = ((size_t)g.N * g.K * (q8 ? 1 : 2) + 255) / 256 * 256;
+  int nrot = (int)std::min<size_t>(32, std::max<size_t>(2, ((size_t)640 << 20) / wstride + 1));
+  char* wrot = nullptr;
+  if (hipMalloc(&wrot, nrot * wstride) != hipSuccess) {
+    (void)hipGetLastError();
+    wrot = nullptr;
+    nrot = 1;
+  }
   auto time_it = [&](Choice c, int reps, float* us) -> int {
-    for (int r = 0; r < 1; r++)
-      if (int rc = launch_choice(t, c, epi, q8, s)) return rc;
+    t.W = wrot ? wrot : g.W;
+    if (int rc = launch_choice(t, c, epi, q8, s)) return rc;
     HI_TRY(hipEventRecord(e0, s));
-    for (int r = 0; r < reps; r++)
+    for (int r = 0; r < reps; r++) {
+      if (wrot) t.W = wrot + (size_t)((r + 1) % nrot) * wstride;
       if (int rc = launch_choice(t, c, epi, q8, s)) return rc;
+    }
     HI_TRY(hipEventRecord(e1, s));
     HI_TRY(hipEventSynchronize(e1));
     float ms = 0.f;
@@ -173,7 +189,7 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
     for (int sp = 1; sp <= 8 && !rc; sp *= 2) {
       if (sp > nkt || (sp > 1 && tiles * sp > 4L * d->cus) || tiles > kMaxTiles) continue;
       float us = 0.f;
-      rc = time_it({c, sp}, 3, &us);
+      rc = time_it({c, sp}, std::max(nrot, 4), &us);
       if (!rc) timed.push_back({us, {c, sp}});
     }
   }
@@ -184,7 +200,7 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
     float best = 1e30f;
     for (size_t f = 0; f < nfin && !rc; f++) {
       float us = 0.f;
-      rc = time_it(timed[f].second, 5, &us);
+      rc = time_it(timed[f].second, std::max(2 * nrot, 8), &us);
       if (!rc && us < best) {
         best = us;
         *out = timed[f].second;
@@ -199,6 +215,7 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
   (void)hipEventDestroy(e1);
   (void)hipStreamSynchronize(s);
   (void)hipFree(scratch);
+  if (wrot) (void)hipFree(wrot);
   if (rc) return rc;
   std::lock_guard<std::mutex> lk(g_tune_mu);
   g_tuned[key] = *out;
@@ -308,7 +325,7 @@ HI_EXPORT int hi_gemm_force_splits(int sp) {
 HI_EXPORT int hi_gemm_num_configs() { return kGemmNumCfgs; }
 HI_EXPORT int hi_gemm_config_desc(int c, char* out, int n) {
   if (c < 0 || c >= kGemmNumCfgs || !out || n < 1) return -1;
-  snprintf(out, n, "mfma 32x32x16 %dx%dx%d waves %dx%d", kGemmCfgs[c].bm, kGemmCfgs[c].bn, kGemmBK, kGemmCfgs[c].wm,
-           kGemmCfgs[c].wn);
+  snprintf(out, n, "mfma 32x32x16 %dx%dx%d waves %dx%d stages %d", kGemmCfgs[c].bm, kGemmCfgs[c].bn, kGemmBK,
+           kGemmCfgs[c].wm, kGemmCfgs[c].wn, kGemmCfgs[c].st);
   return 0;
 }

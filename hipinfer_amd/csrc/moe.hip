@@ -326,9 +326,10 @@ int grouped_gemm(const f16* A, int lda, const f16* W, int64_t wstride_bytes, f16
   g.grp_wstride = wstride_bytes;
   auto fn = gemm_kernel<kGrpBM, kGrpBN, kGemmCfgs[cfg].wm, kGemmCfgs[cfg].wn, kGemmCfgs[cfg].st, EPI, false, true>;
   const size_t lds = gemm_lds_bytes(cfg, false);
-  if (hi_blocks_per_cu(reinterpret_cast<const void*>(fn), kGemmThreads, lds) <= 0) HI_FAIL("moe: grouped GEMM does not fit");
+  constexpr int threads = 64 * kGemmCfgs[cfg].wm * kGemmCfgs[cfg].wn;
+  if (hi_blocks_per_cu(reinterpret_cast<const void*>(fn), threads, lds) <= 0) HI_FAIL("moe: grouped GEMM does not fit");
   const int tiles_n = (N + kGrpBN - 1) / kGrpBN;
-  hipLaunchKernelGGL(fn, dim3(max_row_tiles * tiles_n), dim3(kGemmThreads), lds, s, g);
+  hipLaunchKernelGGL(fn, dim3(max_row_tiles * tiles_n), dim3(threads), lds, s, g);
   HI_TRY(hipGetLastError());
   return 0;
 }
