@@ -284,6 +284,138 @@ def cpu_baseline(torch, model, budget_s=12.0):
                       f"{len(times)} repetitions ({sum(times):.1f} s)"}
 
 
+# ------------------------------------------------------------------ the other BASELINE configs
+def _seeded(torch, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return g
+
+
+def _w(torch, g, N, K, sd=0.02):
+    return torch.empty(N, K, dtype=torch.float16, device="cuda").normal_(0.0, sd, generator=g)
+
+
+def _time(torch, fn, steps):
+    gr = capture(torch, fn)
+    ms, _ = time_graph(torch, gr, steps, 2)
+    del gr
+    return ms
+
+
+def decode_config_bench(torch, hi, name, dims, M_list, n_layers, steps, seed, q8_too=True, bias=False):
+    """A model's decode GEMV set (QKV+RoPE, o + residual, gate/up + SwiGLU, down + residual per layer,
+    then lm_head) over n_layers distinct weight sets, for each row count M: weight GB/s per token."""
+    H, Hq, Hkv, D, I, V = dims
+    g = _seeded(torch, seed)
+    qkv_n = (Hq + 2 * Hkv) * D
+    shapes = {"qkv": (qkv_n, H), "o": (H, Hq * D), "gate_up": (2 * I, H), "down": (H, I)}
+    layers = [{k: _w(torch, g, *sh) for k, sh in shapes.items()} for _ in range(n_layers)]
+    lm = _w(torch, g, V, H)
+    qlayers = [{k: hi.quantize_rows(ly[k]) for k in shapes} for ly in layers] if q8_too else None
+    lm_q = hi.quantize_rows(lm) if q8_too else None
+    nw1 = (torch.rand(H, generator=g, device="cuda") + 0.5).half()
+    nw2 = (torch.rand(H, generator=g, device="cuda") + 0.5).half()
+    b = torch.randn(qkv_n, generator=g, device="cuda").half() if bias else None
+    max_seq = 64
+    ang = torch.arange(max_seq, device="cuda").float()[:, None] * (
+        1.0 / 10000.0 ** (torch.arange(0, D, 2, device="cuda").float() / D))[None, :]
+    cs = torch.stack([ang.cos(), ang.sin()], -1).half().contiguous()
+    wbytes = lambda q8: n_layers * sum(N * K * (1 if q8 else 2) + (2 * N if q8 else 0) for N, K in shapes.values()) + \
+        V * H * (1 if q8 else 2) + (2 * V if q8 else 0)
+    out = {"shapes": {k: list(v) for k, v in shapes.items()}, "lm_head": [V, H], "layers": n_layers, "tokens": {}}
+    for M in M_list:
+        kc = torch.zeros(M, Hkv, max_seq, D, dtype=torch.float16, device="cuda")
+        vc = torch.zeros_like(kc)
+        pos = torch.full((M,), 5, dtype=torch.int32, device="cuda")
+        x0 = torch.randn(M, H, generator=g, device="cuda").half()
+        x = x0.clone()
+        q = torch.empty(M, Hq * D, dtype=torch.float16, device="cuda")
+        act = torch.empty(M, I, dtype=torch.float16, device="cuda")
+        logits = torch.empty(M, V, dtype=torch.float16, device="cuda")
+        for q8 in ([False, True] if q8_too else [False]):
+            def token():
+                x.copy_(x0)
+                for l in range(n_layers):
+                    wsrc = qlayers[l] if q8 else {k: (layers[l][k], None) for k in shapes}
+                    W, sc = wsrc["qkv"]
+                    hi.gemv_qkv_rope(x, W, nw1, Hq, Hkv, cs, pos, kc, vc, q, bias=b, scales=sc)
+                    W, sc = wsrc["o"]
+                    hi.gemv(q, W, out=x, epi=1, scales=sc)
+                    W, sc = wsrc["gate_up"]
+                    hi.gemv(x, W, out=act, normw=nw2, epi=2, scales=sc)
+                    W, sc = wsrc["down"]
+                    hi.gemv(act, W, out=x, epi=1, scales=sc)
+                W, sc = (lm_q if q8 else (lm, None))
+                hi.gemv(x, W, out=logits, normw=nw1, scales=sc)
+            ms = _time(torch, token, steps)
+            wb = wbytes(q8)
+            out["tokens"][f"M{M}_{'int8' if q8 else 'fp16'}"] = {
+                "ms_per_token_set": round(ms, 4), "weight_GB/s": round(wb / (ms * 1e-3) / 1e9, 1),
+                "pct_hbm_peak": round(100 * wb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1), "weight_bytes": wb}
+    del layers, qlayers, lm, lm_q
+    torch.cuda.empty_cache()
+    out["config"] = name
+    return out
+
+
+def moe_bench(torch, hi, steps, seed):
+    """Granite-3.1-1B-A400M-shaped MoE layers (hidden 1024, 32 experts of SwiGLU 1024 -> 2 x 512 and
+    512 -> 1024, top-8, softmax over the top-8 logits, fp16 routing weights, residual scale 0.22) over
+    24 distinct layers: B = 1 decode (router + GEMV experts) and a 256-token prefill (router +
+    grouped MFMA experts)."""
+    H, E, I, k, L = 1024, 32, 512, 8, 24
+    flags = hi.MOE_NORM_TOPK | hi.MOE_FP16_WEIGHTS
+    g = _seeded(torch, seed)
+    Wr = [_w(torch, g, E, H) for _ in range(L)]
+    wgu = [torch.empty(E, 2 * I, H, dtype=torch.float16, device="cuda").normal_(0, 0.02, generator=g) for _ in range(L)]
+    wdn = [torch.empty(E, H, I, dtype=torch.float16, device="cuda").normal_(0, 0.02, generator=g) for _ in range(L)]
+    res = {"config": "Granite-3.1-1B-A400M MoE layer: H 1024, 32 experts (gate/up 1024->2x512, down 512->1024), "
+                     "top-8, 24 distinct layers per step"}
+    for M, path, tag in [(1, 1, "decode_B1_gemv"), (256, 2, "prefill_256_grouped")]:
+        xn = torch.randn(M, H, generator=g, device="cuda").half()
+        x0 = torch.randn(M, H, generator=g, device="cuda").half()
+        x = x0.clone()
+        work = torch.empty(hi.lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device="cuda")
+        idx = torch.empty(M, k, dtype=torch.int32, device="cuda")
+        wts = torch.empty(M, k, dtype=torch.float32, device="cuda")
+
+        def step():
+            x.copy_(x0)
+            for l in range(L):
+                hi.lib.hi_moe_router(hi._p(xn), xn.stride(0), hi._p(Wr[l]), M, E, H, k, flags, hi._p(idx), hi._p(wts),
+                                     hi._s())
+                hi.lib.hi_moe_experts(hi._p(xn), xn.stride(0), hi._p(wgu[l]), hi._p(wdn[l]), hi._p(idx), hi._p(wts), M,
+                                      E, k, H, I, flags, 0.22, hi._p(x), x.stride(0), path, hi._p(work), hi._s())
+        ms = _time(torch, step, steps)
+        us = ms * 1e3 / L
+        if M == 1:
+            used = idx.unique().numel()
+            b = E * H * 2 + used * (2 * I * H + H * I) * 2
+            res[tag] = {"us_per_layer": round(us, 2), "experts_read": used, "bytes_per_layer": b,
+                        "GB/s": round(b / us / 1e3, 1), "pct_hbm_peak": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 1)}
+        else:
+            flops = 2.0 * M * k * (2 * I * H + H * I) + 2.0 * M * E * H
+            res[tag] = {"us_per_layer": round(us, 2), "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1),
+                        "expert_pairs": M * k}
+    del Wr, wgu, wdn
+    torch.cuda.empty_cache()
+    return res
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE runs, each scaled by the same counter's reading for a plain copy of
+    known size). None when the summary is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_gate_up_llama31_8b_hbm_bytes.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -292,6 +424,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-int8", action="store_true")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM (C3) section")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C4 / C5 sections")
     ap.add_argument("--profile", choices=["gate_up", "token", "gemm"], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
     args = ap.parse_args()
@@ -384,13 +517,25 @@ def main():
         res["int8"] = {"value": round(v8, 1), "unit": "GB/s", "ms_per_step": round(out["int8"][0], 4),
                        "pct_hbm_peak": round(100 * v8 / HBM_PEAK_GBS, 2), "weight_bytes_per_step": wb8}
     res["kernels"] = kernels
+    roofline["traffic"] = traffic_from_profile()
+    roofline["traffic_source"] = "profiles/gemv_gate_up_llama31_8b_hbm_bytes.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)"
     res["roofline"] = roofline
     if not args.no_gemm:
+        log("prefill GEMM ...")
+        res["prefill_gemm"] = prefill_bench(torch, hi, args.steps, args.warmup, not args.no_int8)
+    if not args.no_configs:
         del g16
         if "int8" in out:
             del g8
-        log("prefill GEMM ...")
-        res["prefill_gemm"] = prefill_bench(torch, hi, args.steps, args.warmup, not args.no_int8)
+        log("other configs ...")
+        res["configs"] = {
+            "C1_tinyllama": decode_config_bench(torch, hi, "TinyLlama-1.1B decode GEMV set (22 distinct layers)",
+                                                (2048, 32, 4, 64, 5632, 32000), [1], 22, args.steps, SEED + 10),
+            "C4_qwen25_1p5b": decode_config_bench(torch, hi, "Qwen2.5-1.5B decode/verify GEMV set with QKV bias "
+                                                  "(28 distinct layers), N rows", (1536, 12, 2, 128, 8960, 151936),
+                                                  [1, 2, 5, 8], 28, args.steps, SEED + 11, bias=True),
+            "C5_granite_moe": moe_bench(torch, hi, args.steps, SEED + 12),
+        }
     if not args.no_cpu:
         log("cpu baseline ...")
         res["cpu_baseline"] = cpu_baseline(torch, model)
