@@ -10,7 +10,9 @@
 //    combines) and streams it with 128-bit nontemporal loads (the weights are read once), lane l
 //    taking 16-byte chunks l, l+64, ...; the first unit's loads are issued before the activation
 //    prologue and every next unit's before the current unit's reduction, so the prologue and the
-//    reductions hide under weight traffic;
+//    reductions hide under weight traffic; a unit's epilogue inputs (row scales, residual, bias,
+//    RoPE table entry) are read right after its first weights, so the epilogue waits for no
+//    dependent memory round trip;
 //  * int8 chunks are unpacked to exact fp16 in registers (v_perm_b32 + one packed fp16 sub per
 //    two weights) and every pair of weights meets its activation pair in one v_dot2_f32_f16
 //    (fp32 accumulate);
@@ -99,6 +101,32 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
     }
   };
 
+  // Epilogue inputs of a unit (row scales, residual, bias, RoPE table entry), read right after the
+  // unit's first weights so that none of them is a dependent memory round trip at the end of the
+  // unit; kept as the raw loaded values. Lane m < M reads those of activation row m.
+  struct Pre {
+    f16 s0, s1, r, b0, b1;
+    f16x2 cs;
+  };
+  const bool epi_lane = lane < MR && lane < M;
+  const int my_pos = (EPI == 3 && epi_lane) ? a.pos[lane] : 0;
+  auto load_pre = [&](Pre& pre, int u, const int (&rows)[NR]) {
+    if (!epi_lane) return;
+    if constexpr (WF != WF_F16) {
+      pre.s0 = a.scales[rows[0]];
+      pre.s1 = a.scales[rows[NR - 1]];
+    }
+    if constexpr (EPI == 1) pre.r = a.out[lane * a.ldo + u];
+    if constexpr (EPI == 3) {
+      const int HD = a.D >> 1;
+      if (a.bias) {
+        pre.b0 = a.bias[rows[0]];
+        pre.b1 = a.bias[rows[NR - 1]];
+      }
+      pre.cs = a.cs[(int64_t)my_pos * HD + u % HD];
+    }
+  };
+
   // ---- 1. activation (and norm-weight) chunks into registers, before any weight load, so
   //         their latency overlaps the first weight step's
   const bool xreg = XC > 0 && K8 <= XC * kGemvThreads;
@@ -117,11 +145,13 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   // ---- 2. the first step of this wave's first unit
   LT wv[NR][U];
   int rows[NR];
+  Pre pn{};  // the epilogue inputs of the unit whose first step is in flight
   const int u0 = blockIdx.x * kGemvWaves + wave;
   bool have = u0 < n_units;
   if (have) {
     unit_rows(u0, rows);
     load_step(wv, rows, 0);
+    load_pre(pn, u0, rows);
   }
   // ---- 3. stage the activation rows in LDS, RMSNorm'd (HF order) when normw is given; rows >= M
   //         are zero so no garbage reaches the sums
@@ -220,6 +250,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
 
   // ---- 4. stream the units; each unit's next-unit prefetch is issued before its reduction
   for (int u = u0; u < n_units; u += nw) {
+    const Pre pc = pn;
     float acc[NR][MR];
 #pragma unroll
     for (int j = 0; j < NR; j++)
@@ -261,12 +292,10 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
       }
     }
 
-    int cur[NR];
-#pragma unroll
-    for (int j = 0; j < NR; j++) cur[j] = rows[j];
     if (u + nw < n_units) {
       unit_rows(u + nw, rows);
       load_step(wv, rows, 0);
+      load_pre(pn, u + nw, rows);
       have = true;
     }
 
@@ -275,7 +304,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int m = 0; m < MR; m++) acc[j][m] = wave_sum(acc[j][m]);
 
-    if (lane < MR && lane < M) {
+    if (epi_lane) {
       float a0 = 0.f, a1 = 0.f;  // this lane's row, selected without dynamic register indexing
 #pragma unroll
       for (int m = 0; m < MR; m++)
@@ -284,26 +313,26 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
           a1 = acc[NR - 1][m];
         }
       if constexpr (WF != WF_F16) {
-        a0 *= (float)a.scales[cur[0]];
-        a1 *= (float)a.scales[cur[NR - 1]];
+        a0 *= (float)pc.s0;  // the row scale applied once to the reduced sum (reference kernels.cuh:261)
+        a1 *= (float)pc.s1;
       }
       f16* orow = a.out + lane * a.ldo;
       if constexpr (EPI == 0) {
         orow[u] = (f16)a0;
       } else if constexpr (EPI == 1) {
-        orow[u] = orow[u] + (f16)a0;  // fp16 add, correctly rounded
+        orow[u] = pc.r + (f16)a0;  // fp16 add, correctly rounded
       } else if constexpr (EPI == 2) {
         orow[u] = silu_mul(a0, a1);
       } else {
         const int D = a.D, HD = D >> 1, head = u / HD, d = u - head * HD;
-        const int p = a.pos[lane];
+        const int p = my_pos;
         const int slot = a.kv_slot >= 0 ? a.kv_slot : a.slot_base + lane;
         if (a.bias) {
-          a0 += (float)a.bias[cur[0]];
-          a1 += (float)a.bias[cur[NR - 1]];
+          a0 += (float)pc.b0;
+          a1 += (float)pc.b1;
         }
         f16 y1 = (f16)a0, y2 = (f16)a1;
-        if (head < a.Hq + a.Hkv) rope_pair(y1, y2, a.cs[(int64_t)p * HD + d]);
+        if (head < a.Hq + a.Hkv) rope_pair(y1, y2, pc.cs);
         f16* dst;
         if (head < a.Hq) dst = orow + head * D;
         else if (head < a.Hq + a.Hkv) dst = a.kc + (((int64_t)slot * a.Hkv + head - a.Hq) * a.max_seq + p) * D;
