@@ -425,7 +425,7 @@ def main():
     ap.add_argument("--no-int8", action="store_true")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM (C3) section")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C4 / C5 sections")
-    ap.add_argument("--profile", choices=["gate_up", "token", "gemm"], default=None,
+    ap.add_argument("--profile", choices=["gate_up", "token", "gemm", "moe"], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -440,6 +440,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     log(f"device: {torch.cuda.get_device_name(0)}, {hi.lib.hi_device_cus()} CUs")
+    if args.profile == "moe":
+        log(json.dumps(moe_bench(torch, hi, args.steps, SEED + 12)))
+        return
     t0 = time.perf_counter()
     model = Model(torch, hi, q8_too=not args.no_int8)
     log(f"weights ready in {time.perf_counter() - t0:.1f} s")

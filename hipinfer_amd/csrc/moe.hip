@@ -12,7 +12,9 @@
 // Two expert paths, as the reference:
 //  * GEMV (decode, few rows): one wave per (pair, unit) streams the selected experts' gate/up
 //    rows; one wave per (token, hidden column) does the k down-projection dot products and the
-//    weighted combine in slot order. Fixed launch shape, the expert choice stays on the device.
+//    weighted combine in slot order. Each wave issues all the loads of a round together (a round
+//    covers a whole row at the usual sizes), so a kernel costs about one memory round trip.
+//    Fixed launch shape, the expert choice stays on the device.
 //  * grouped (prefill): a counting sort of the M*k (token, slot) pairs by expert, which also
 //    writes each expert's row-tile prefix; a gather; two grouped MFMA GEMM launches (gate/up with
 //    the SwiGLU epilogue, then down) in which every block finds its expert from the prefix; and
@@ -39,70 +41,76 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float best, int bi
 }
 
 // ------------------------------------------------------------------ router
-__global__ void __launch_bounds__(256) moe_router_kernel(const f16* __restrict__ xn, int64_t ldx,
-                                                         const f16* __restrict__ Wr, int E, int H, int k, int flags,
-                                                         int* __restrict__ idx_out, float* __restrict__ w_out) {
+// One block of 16 waves per token row; each wave computes two experts' logits with all the row's
+// loads issued together (CH chunks of 8 halves per lane per round), so a row costs about one memory
+// round trip. The top k are then chosen by rank: argmax_better is a strict total order on (logit,
+// index), so the expert that exactly j others beat is the j-th pick of the sequential argmax, and
+// every expert's rank is counted in parallel from the logits in LDS.
+constexpr int kRouterWaves = 16;
+template <int CH>
+__global__ void __launch_bounds__(kRouterWaves * 64) moe_router_kernel(const f16* __restrict__ xn, int64_t ldx,
+                                                                      const f16* __restrict__ Wr, int E, int H, int k,
+                                                                      int flags, int* __restrict__ idx_out,
+                                                                      float* __restrict__ w_out) {
   __shared__ float logit[kMoeMaxE];
   __shared__ float selv[kMoeMaxK];
   __shared__ int seli[kMoeMaxK];
   const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const f16* xr = xn + t * ldx;
-  for (int e = wave; e < E; e += 4) {
-    const f16* wr = Wr + (int64_t)e * H;
-    float acc = 0.f;
-    for (int c = lane; c < H / 8; c += 64) {
-      const u32x4 a = *reinterpret_cast<const u32x4*>(xr + 8 * c), b = *reinterpret_cast<const u32x4*>(wr + 8 * c);
+  const int H8 = H / 8;
+  for (int e0 = wave; e0 < E; e0 += 2 * kRouterWaves) {
+    const int e1 = e0 + kRouterWaves;
+    const f16* w0 = Wr + (int64_t)e0 * H;
+    const f16* w1 = Wr + (int64_t)min(e1, E - 1) * H;
+    float a0 = 0.f, a1 = 0.f;
+    for (int g = 0; g < H8; g += 64 * CH) {
+      u32x4 xv[CH], v0[CH], v1[CH];
 #pragma unroll
-      for (int p = 0; p < 4; p++) acc = dot2(as_h2(a[p]), as_h2(b[p]), acc);
+      for (int j = 0; j < CH; j++) {
+        const int c = g + j * 64 + lane;
+        const int cc = c < H8 ? c : 0;  // past the row: a valid chunk, zeroed below
+        xv[j] = *reinterpret_cast<const u32x4*>(xr + 8 * cc);
+        v0[j] = *reinterpret_cast<const u32x4*>(w0 + 8 * cc);
+        v1[j] = *reinterpret_cast<const u32x4*>(w1 + 8 * cc);
+      }
+#pragma unroll
+      for (int j = 0; j < CH; j++) {
+        const bool ok = g + j * 64 + lane < H8;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+          const f16x2 x2 = as_h2(ok ? xv[j][p] : 0u);
+          a0 = dot2(as_h2(v0[j][p]), x2, a0);
+          a1 = dot2(as_h2(v1[j][p]), x2, a1);
+        }
+      }
     }
-    acc = wave_sum(acc);
-    if (lane == 0) logit[e] = (float)(f16)acc;  // the router linear is rounded to fp16
+    a0 = wave_sum(a0);
+    a1 = wave_sum(a1);
+    if (lane == 0) {
+      logit[e0] = (float)(f16)a0;  // the router linear is rounded to fp16
+      if (e1 < E) logit[e1] = (float)(f16)a1;
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kRouterWaves * 64) {
+    const float v = logit[e];
+    int r = 0;
+#pragma unroll 8
+    for (int o = 0; o < E; o++) r += argmax_better(logit[o], o, v, e);
+    if (r < k) {
+      seli[r] = e;
+      selv[r] = v;
+    }
   }
   __syncthreads();
   if (wave != 0) return;
-  float v[kMoeMaxE / 64];
-#pragma unroll
-  for (int i = 0; i < kMoeMaxE / 64; i++) {
-    const int e = i * 64 + lane;
-    v[i] = e < E ? logit[e] : -__builtin_huge_valf();
-  }
-  unsigned taken = 0;  // bit i: this lane's expert i * 64 + lane is selected
-  for (int j = 0; j < k; j++) {
-    float best = -__builtin_huge_valf();
-    int bi = 0x7fffffff;  // above every expert index: any untaken expert beats it
-#pragma unroll
-    for (int i = 0; i < kMoeMaxE / 64; i++) {
-      const int e = i * 64 + lane;
-      if (e < E && !((taken >> i) & 1u) && argmax_better(v[i], e, best, bi)) {
-        best = v[i];
-        bi = e;
-      }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(best, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (argmax_better(ov, oi, best, bi)) {
-        best = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);  // every lane holds the winner; its owner marks it
-    if (lane == 0) {
-      seli[j] = bi;
-      selv[j] = best;
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   const float mx = selv[0];
   float denom = 0.f;
   if (flags & kMoeNormTopk) {
     for (int j = 0; j < k; j++) denom += expf(selv[j] - mx);
   } else {
     float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < kMoeMaxE / 64; i++)
-      if (i * 64 + lane < E) sum += expf(v[i] - mx);
+    for (int e = lane; e < E; e += 64) sum += expf(logit[e] - mx);
     denom = wave_sum(sum);
   }
   if (lane < k) {
@@ -113,110 +121,113 @@ __global__ void __launch_bounds__(256) moe_router_kernel(const f16* __restrict__
   }
 }
 
+// Chunks of 8 halves per lane per load round for a row of n halves: one round covers the row up to
+// n = 64 * 8 * 4.
+inline int chunks_for(int n) { return n <= 512 ? 1 : n <= 1024 ? 2 : 4; }
+
 // ------------------------------------------------------------------ GEMV expert path
-// Gate/up + SwiGLU: block (x, pair p) covers 16 units; wave w takes units 4w..4w+3 of them. Unit o
-// of expert e reads rows (o/16)*32 + o%16 and that + 16 of wgu[e] [2I, H].
-constexpr int kGuUnitsPerWave = 4;
-__global__ void __launch_bounds__(256) moe_gemv_gu_kernel(const f16* __restrict__ xn, int64_t ldx,
-                                                          const f16* __restrict__ wgu, const int* __restrict__ idx,
-                                                          int k, int E, int H, int I, f16* __restrict__ act) {
-  const int p = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Gate/up + SwiGLU: one wave per (token-slot pair p, output unit o); unit o of expert e reads rows
+// (o/16)*32 + o%16 and that + 16 of wgu[e] [2I, H]. A round issues both rows' and the activation's
+// chunks together (CH per lane), so a unit of H <= 64 * 8 * CH costs one round trip.
+constexpr int kMoeWaves = 8;
+template <int CH>
+__global__ void __launch_bounds__(kMoeWaves * 64) moe_gemv_gu_kernel(const f16* __restrict__ xn, int64_t ldx,
+                                                                     const f16* __restrict__ wgu,
+                                                                     const int* __restrict__ idx, int n, int k, int E,
+                                                                     int H, int I, f16* __restrict__ act) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * kMoeWaves + (threadIdx.x >> 6);
+  if (w >= (int64_t)n * I) return;
+  const int p = (int)(w / I), o = (int)(w - (int64_t)p * I);
   const int e = idx[p];
-  const int o0 = (blockIdx.x * 4 + wave) * kGuUnitsPerWave;
   if (e < 0 || e >= E) {  // no expert: this slot's activation is zero
-    if (lane < kGuUnitsPerWave && o0 + lane < I) act[(int64_t)p * I + o0 + lane] = (f16)0.f;
+    if (lane == 0) act[(int64_t)p * I + o] = (f16)0.f;
     return;
   }
-  const f16* W = wgu + (int64_t)e * 2 * I * H;
+  const int r0 = (o >> 4) * 32 + (o & 15);
+  const f16* g = wgu + ((int64_t)e * 2 * I + r0) * H;
+  const f16* u = g + 16 * (int64_t)H;
   const f16* xr = xn + (int64_t)(p / k) * ldx;
-  float acc[kGuUnitsPerWave][2];
-  const f16* rows[kGuUnitsPerWave][2];
+  const int H8 = H / 8;
+  float ag = 0.f, au = 0.f;
+  for (int b = 0; b < H8; b += 64 * CH) {
+    u32x4 xv[CH], gv[CH], uv[CH];
 #pragma unroll
-  for (int u = 0; u < kGuUnitsPerWave; u++) {
-    const int o = min(o0 + u, I - 1);
-    const int r0 = (o >> 4) * 32 + (o & 15);
-    rows[u][0] = W + (int64_t)r0 * H;
-    rows[u][1] = W + (int64_t)(r0 + 16) * H;
-    acc[u][0] = acc[u][1] = 0.f;
+    for (int j = 0; j < CH; j++) {
+      const int c = b + j * 64 + lane, cc = c < H8 ? c : 0;
+      xv[j] = *reinterpret_cast<const u32x4*>(xr + 8 * cc);
+      gv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g + 8 * cc));
+      uv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(u + 8 * cc));
+    }
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+      const bool ok = b + j * 64 + lane < H8;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const f16x2 x2 = as_h2(ok ? xv[j][q] : 0u);
+        ag = dot2(as_h2(gv[j][q]), x2, ag);
+        au = dot2(as_h2(uv[j][q]), x2, au);
+      }
+    }
   }
-  for (int c = lane; c < H / 8; c += 64) {
-    const u32x4 xv = *reinterpret_cast<const u32x4*>(xr + 8 * c);
-    u32x4 wv[kGuUnitsPerWave][2];
-#pragma unroll
-    for (int u = 0; u < kGuUnitsPerWave; u++)
-#pragma unroll
-      for (int r = 0; r < 2; r++) wv[u][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows[u][r] + 8 * c));
-#pragma unroll
-    for (int u = 0; u < kGuUnitsPerWave; u++)
-#pragma unroll
-      for (int r = 0; r < 2; r++)
-#pragma unroll
-        for (int q = 0; q < 4; q++) acc[u][r] = dot2(as_h2(wv[u][r][q]), as_h2(xv[q]), acc[u][r]);
-  }
-#pragma unroll
-  for (int u = 0; u < kGuUnitsPerWave; u++) {
-    const float g = wave_sum(acc[u][0]), up = wave_sum(acc[u][1]);
-    if (lane == 0 && o0 + u < I) act[(int64_t)p * I + o0 + u] = silu_mul(g, up);
-  }
+  ag = wave_sum(ag);
+  au = wave_sum(au);
+  if (lane == 0) act[(int64_t)p * I + o] = silu_mul(ag, au);
 }
 
-// Down projection + weighted combine + residual: wave (token b, column h) computes the k dot
-// products wdown[e_j][h] . act[b*k + j] four at a time and adds them up in slot order.
-constexpr int kDownColsPerWave = 2;
-__global__ void __launch_bounds__(256) moe_gemv_down_kernel(const f16* __restrict__ act, const f16* __restrict__ wdown,
-                                                            const int* __restrict__ idx, const float* __restrict__ wts,
-                                                            int k, int E, int H, int I, int flags, float scale, f16* x,
-                                                            int64_t ldx) {
-  const int b = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int h0 = (blockIdx.x * 4 + wave) * kDownColsPerWave;
-  float sum[kDownColsPerWave];
+// Down projection + weighted combine + residual: one wave per (token b, hidden column h). All k
+// (expert row, activation row) chunk pairs of a round are loaded together; the k dot products are
+// then reduced one by one and combined in slot order. KM >= k bounds the per-wave registers.
+template <int KM>
+__global__ void __launch_bounds__(kMoeWaves * 64) moe_gemv_down_kernel(const f16* __restrict__ act,
+                                                                       const f16* __restrict__ wdown,
+                                                                       const int* __restrict__ idx,
+                                                                       const float* __restrict__ wts, int M, int k,
+                                                                       int E, int H, int I, int flags, float scale,
+                                                                       f16* x, int64_t ldx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * kMoeWaves + (threadIdx.x >> 6);
+  if (w >= (int64_t)M * H) return;
+  const int b = (int)(w / H), h = (int)(w - (int64_t)b * H);
+  int ex[KM];
 #pragma unroll
-  for (int u = 0; u < kDownColsPerWave; u++) sum[u] = 0.f;
-  for (int j0 = 0; j0 < k; j0 += 4) {
-    float acc[4][kDownColsPerWave];
-    int ex[4];
+  for (int j = 0; j < KM; j++) ex[j] = j < k ? idx[(int64_t)b * k + j] : -1;
+  float acc[KM];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      ex[r] = j0 + r < k ? idx[(int64_t)b * k + j0 + r] : -1;
+  for (int j = 0; j < KM; j++) acc[j] = 0.f;
+  const int I8 = I / 8;
+  for (int c0 = 0; c0 < I8; c0 += 64) {
+    const int c = c0 + lane, cc = c < I8 ? c : 0;
+    u32x4 wv[KM], av[KM];
 #pragma unroll
-      for (int u = 0; u < kDownColsPerWave; u++) acc[r][u] = 0.f;
-    }
-    for (int c = lane; c < I / 8; c += 64) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        if (ex[r] < 0 || ex[r] >= E) continue;
-        const u32x4 av = *reinterpret_cast<const u32x4*>(act + ((int64_t)b * k + j0 + r) * I + 8 * c);
-#pragma unroll
-        for (int u = 0; u < kDownColsPerWave; u++) {
-          const int h = min(h0 + u, H - 1);
-          const u32x4 wv = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4*>(wdown + ((int64_t)ex[r] * H + h) * I + 8 * c));
-#pragma unroll
-          for (int q = 0; q < 4; q++) acc[r][u] = dot2(as_h2(wv[q]), as_h2(av[q]), acc[r][u]);
-        }
+    for (int j = 0; j < KM; j++) {
+      if (j < k) {
+        const int e = (ex[j] >= 0 && ex[j] < E) ? ex[j] : 0;  // an id outside [0, E) is dropped below
+        wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wdown + ((int64_t)e * H + h) * I + 8 * cc));
+        av[j] = *reinterpret_cast<const u32x4*>(act + ((int64_t)b * k + j) * I + 8 * cc);
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      if (ex[r] < 0 || ex[r] >= E) continue;  // uniform over the wave
-      const float wr = wts[(int64_t)b * k + j0 + r];
+    for (int j = 0; j < KM; j++) {
+      if (j < k) {
 #pragma unroll
-      for (int u = 0; u < kDownColsPerWave; u++) {
-        const float c = (float)(f16)wave_sum(acc[r][u]) * wr;
-        sum[u] += (flags & kMoeFp16Weights) ? (float)(f16)c : c;
+        for (int q = 0; q < 4; q++) acc[j] = dot2(as_h2(wv[j][q]), as_h2(c < I8 ? av[j][q] : 0u), acc[j]);
       }
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < KM; j++) {
+    if (j < k && ex[j] >= 0 && ex[j] < E) {  // uniform over the wave
+      const float c = (float)(f16)wave_sum(acc[j]) * wts[(int64_t)b * k + j];
+      sum += (flags & kMoeFp16Weights) ? (float)(f16)c : c;
     }
   }
   if (lane == 0) {
-#pragma unroll
-    for (int u = 0; u < kDownColsPerWave; u++) {
-      const int h = h0 + u;
-      if (h >= H) continue;
-      f16 o = (f16)sum[u];
-      if (scale != 1.f) o = (f16)((float)o * scale);
-      f16* dst = x + (int64_t)b * ldx + h;
-      *dst = *dst + o;
-    }
+    f16 o = (f16)sum;
+    if (scale != 1.f) o = (f16)((float)o * scale);
+    f16* dst = x + (int64_t)b * ldx + h;
+    *dst = *dst + o;
   }
 }
 
@@ -355,7 +366,9 @@ HI_EXPORT int hi_moe_router(const void* xn, int ldx, const void* Wr, int M, int 
   if (M == 0) return 0;
   if (!xn || !Wr || !idx || !w || ((uintptr_t)xn & 15) || ((uintptr_t)Wr & 15) || ldx % 8)
     HI_FAIL("hi_moe_router: xn and Wr must be 16-byte aligned device pointers (ldx %% 8 == 0)");
-  hipLaunchKernelGGL(moe_router_kernel, dim3(M), dim3(256), 0, (hipStream_t)s, (const f16*)xn, (int64_t)ldx,
+  const auto kern = chunks_for(H) == 1 ? moe_router_kernel<1> : chunks_for(H) == 2 ? moe_router_kernel<2>
+                                                                                     : moe_router_kernel<4>;
+  hipLaunchKernelGGL(kern, dim3(M), dim3(kRouterWaves * 64), 0, (hipStream_t)s, (const f16*)xn, (int64_t)ldx,
                      (const f16*)Wr, E, H, k, flags, idx, w);
   HI_TRY(hipGetLastError());
   return 0;
@@ -398,11 +411,15 @@ HI_EXPORT int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const vo
   const f16* Wgu = (const f16*)wgu;
   const f16* Wd = (const f16*)wdown;
   if (path == 1 || (path == 0 && M <= gemv_max())) {
-    hipLaunchKernelGGL(moe_gemv_gu_kernel, dim3((I + 4 * kGuUnitsPerWave - 1) / (4 * kGuUnitsPerWave), n), dim3(256), 0,
-                       st, (const f16*)xn, (int64_t)ldxn, Wgu, idx, k, E, H, I, act);
+    const int64_t gu_waves = (int64_t)n * I, dn_waves = (int64_t)M * H;
+    const auto gu = chunks_for(H) == 1 ? moe_gemv_gu_kernel<1> : chunks_for(H) == 2 ? moe_gemv_gu_kernel<2>
+                                                                                    : moe_gemv_gu_kernel<4>;
+    hipLaunchKernelGGL(gu, dim3((unsigned)((gu_waves + kMoeWaves - 1) / kMoeWaves)), dim3(kMoeWaves * 64),
+                       0, st, (const f16*)xn, (int64_t)ldxn, Wgu, idx, n, k, E, H, I, act);
     HI_TRY(hipGetLastError());
-    hipLaunchKernelGGL(moe_gemv_down_kernel, dim3((H + 4 * kDownColsPerWave - 1) / (4 * kDownColsPerWave), M), dim3(256),
-                       0, st, act, Wd, idx, w, k, E, H, I, flags, scale, (f16*)x, (int64_t)ldx);
+    const auto dn = k <= 4 ? moe_gemv_down_kernel<4> : k <= 8 ? moe_gemv_down_kernel<8> : moe_gemv_down_kernel<16>;
+    hipLaunchKernelGGL(dn, dim3((unsigned)((dn_waves + kMoeWaves - 1) / kMoeWaves)),
+                       dim3(kMoeWaves * 64), 0, st, act, Wd, idx, w, M, k, E, H, I, flags, scale, (f16*)x, (int64_t)ldx);
     HI_TRY(hipGetLastError());
     return 0;
   }

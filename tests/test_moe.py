@@ -35,7 +35,8 @@ def rn(r, *shape, s=1.0):
 
 
 LAYERS = [("granite-like", 32, 8, 1024, 512, 3, 0.22), ("mixtral-like", 8, 2, 512, 1024, 1, 1.0),
-          ("olmoe-like", 64, 8, 2048, 1024, 2, 1.0)]
+          ("olmoe-like", 64, 8, 2048, 1024, 2, 1.0), ("max-k", 128, 16, 512, 256, 1, 1.0),
+          ("max-e", 256, 4, 256, 128, 3, 1.0)]
 
 
 @pytest.mark.parametrize("name,E,k,H,I,flags,scale", LAYERS, ids=[l[0] for l in LAYERS])
