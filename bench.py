@@ -425,7 +425,8 @@ def main():
     ap.add_argument("--no-int8", action="store_true")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM (C3) section")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C4 / C5 sections")
-    ap.add_argument("--profile", choices=["gate_up", "token", "gemm", "moe"], default=None,
+    ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe"] +
+                    [k + q for k in ("qkv", "o", "gate_up", "down", "lm_head") for q in ("", "8")], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -453,7 +454,9 @@ def main():
             b = pm.buffers(1024)
             fn = lambda: pm.layer_pass(b, False)
         else:
-            fn = (lambda: model.one_kind("gate_up", False)) if args.profile == "gate_up" else (lambda: model.token(False))
+            q8 = args.profile.endswith("8")
+            kind = args.profile.rstrip("8")
+            fn = (lambda: model.token(q8)) if kind == "token" else (lambda: model.one_kind(kind, q8))
         g = capture(torch, fn)
         for _ in range(args.steps):
             g.replay()
