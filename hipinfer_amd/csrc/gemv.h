@@ -53,13 +53,14 @@ template <> struct WLoad<WF_I8H> { typedef u32x2 T; };
 constexpr int kGemvThreads = 512;              // 8 waves per block
 constexpr int kGemvWaves = kGemvThreads / kWave;
 
-template <int MR, bool NORM, int EPI, int WF>
+template <int MR, bool NORM, int EPI, int WF, int G>
 __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   constexpr int NR = EPI >= 2 ? 2 : 1;                  // weight rows per output unit
+  constexpr int R = NR * G;                             // weight rows per item (G consecutive units)
   constexpr int WPL = WF == WF_I8 ? 16 : 8;             // weights per load
   constexpr int XPL = WPL / 8;                          // 16-byte activation chunks per load
   constexpr int WB = WF == WF_F16 ? 16 : WPL;           // bytes per load
-  constexpr int U = 8 / NR;                             // loads per row per step (128 B per lane)
+  constexpr int U = R >= 8 ? 1 : 8 / R;                 // loads per row per step (8 per lane in flight)
   constexpr int XC = MR <= 8 ? (MR <= 4 ? 4 / MR : 1) : 0;  // activation chunks per row held in registers
   typedef typename WLoad<WF>::T LT;
   extern __shared__ u32x4 xs[];                         // [MR][K / 8] activation chunks
@@ -68,31 +69,38 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = a.K, K8 = K >> 3, M = a.M;
   const int n_units = EPI >= 2 ? a.N / 2 : a.N;
+  const int n_items = (n_units + G - 1) / G;
   const int nload = K / WPL;
   const int64_t row_bytes = (int64_t)K * (WF == WF_F16 ? 2 : 1);
   const char* Wb = reinterpret_cast<const char*>(a.W);
   const int nw = gridDim.x * kGemvWaves;
 
-  auto unit_rows = [&](int u, int (&rows)[NR]) {
-    if constexpr (EPI <= 1) {
-      rows[0] = u;
-    } else if constexpr (EPI == 2) {  // gate/up interleaved in groups of 16 rows
-      rows[0] = (u >> 4) * 32 + (u & 15);
-      rows[NR - 1] = rows[0] + 16;
-    } else {  // rows d and d + D/2 of one head
-      const int HD = a.D >> 1;
-      rows[0] = (u / HD) * a.D + u % HD;
-      rows[NR - 1] = rows[0] + HD;
+  // The R weight rows of item t: units t*G .. t*G+G-1 (a unit past the end repeats the last one;
+  // its results are never stored).
+  auto item_rows = [&](int t, int (&rows)[R]) {
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      const int u = min(t * G + g, n_units - 1);
+      if constexpr (EPI <= 1) {
+        rows[g] = u;
+      } else if constexpr (EPI == 2) {  // gate/up interleaved in groups of 16 rows
+        rows[2 * g] = (u >> 4) * 32 + (u & 15);
+        rows[2 * g + 1] = rows[2 * g] + 16;
+      } else {  // rows d and d + D/2 of one head
+        const int HD = a.D >> 1;
+        rows[2 * g] = (u / HD) * a.D + u % HD;
+        rows[2 * g + 1] = rows[2 * g] + HD;
+      }
     }
   };
-  // One step of a unit: U 16-byte (or 8-byte) chunks of each of its rows, streamed past the
+  // One step of an item: U 16-byte (or 8-byte) chunks of each of its rows, streamed past the
   // caches (nontemporal: the weights are read exactly once).
-  auto load_step = [&](LT (&wv)[NR][U], const int (&rows)[NR], int base) {
+  auto load_step = [&](LT (&wv)[R][U], const int (&rows)[R], int base) {
 #pragma unroll
     for (int i = 0; i < U; i++) {
       const int c = base + i * 64 + lane;
 #pragma unroll
-      for (int j = 0; j < NR; j++) {
+      for (int j = 0; j < R; j++) {
         if (c < nload)
           wv[j][i] = __builtin_nontemporal_load(reinterpret_cast<const LT*>(Wb + rows[j] * row_bytes + (int64_t)c * WB));
         else
@@ -101,29 +109,33 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
     }
   };
 
-  // Epilogue inputs of a unit (row scales, residual, bias, RoPE table entry), read right after the
-  // unit's first weights so that none of them is a dependent memory round trip at the end of the
-  // unit; kept as the raw loaded values. Lane m < M reads those of activation row m.
+  // Epilogue inputs of an item's units (row scales, residual, bias, RoPE table entry), read right
+  // after the item's first weights so that none of them is a dependent memory round trip at the
+  // end of the item; kept as the raw loaded values. Lane m < M reads those of activation row m.
   struct Pre {
     f16 s0, s1, r, b0, b1;
     f16x2 cs;
   };
   const bool epi_lane = lane < MR && lane < M;
   const int my_pos = (EPI == 3 && epi_lane) ? a.pos[lane] : 0;
-  auto load_pre = [&](Pre& pre, int u, const int (&rows)[NR]) {
+  auto load_pre = [&](Pre (&pre)[G], int t, const int (&rows)[R]) {
     if (!epi_lane) return;
-    if constexpr (WF != WF_F16) {
-      pre.s0 = a.scales[rows[0]];
-      pre.s1 = a.scales[rows[NR - 1]];
-    }
-    if constexpr (EPI == 1) pre.r = a.out[lane * a.ldo + u];
-    if constexpr (EPI == 3) {
-      const int HD = a.D >> 1;
-      if (a.bias) {
-        pre.b0 = a.bias[rows[0]];
-        pre.b1 = a.bias[rows[NR - 1]];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      const int u = min(t * G + g, n_units - 1);
+      if constexpr (WF != WF_F16) {
+        pre[g].s0 = a.scales[rows[g * NR]];
+        pre[g].s1 = a.scales[rows[g * NR + NR - 1]];
       }
-      pre.cs = a.cs[(int64_t)my_pos * HD + u % HD];
+      if constexpr (EPI == 1) pre[g].r = a.out[lane * a.ldo + u];
+      if constexpr (EPI == 3) {
+        const int HD = a.D >> 1;
+        if (a.bias) {
+          pre[g].b0 = a.bias[rows[g * NR]];
+          pre[g].b1 = a.bias[rows[g * NR + NR - 1]];
+        }
+        pre[g].cs = a.cs[(int64_t)my_pos * HD + u % HD];
+      }
     }
   };
 
@@ -142,16 +154,16 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
         xr[m][j] = (c < K8 && m < M) ? *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c) : u32x4{0u, 0u, 0u, 0u};
     }
   }
-  // ---- 2. the first step of this wave's first unit
-  LT wv[NR][U];
-  int rows[NR];
-  Pre pn{};  // the epilogue inputs of the unit whose first step is in flight
-  const int u0 = blockIdx.x * kGemvWaves + wave;
-  bool have = u0 < n_units;
+  // ---- 2. the first step of this wave's first item
+  LT wv[R][U];
+  int rows[R];
+  Pre pn[G] = {};  // the epilogue inputs of the item whose first step is in flight
+  const int t0 = blockIdx.x * kGemvWaves + wave;
+  bool have = t0 < n_items;
   if (have) {
-    unit_rows(u0, rows);
+    item_rows(t0, rows);
     load_step(wv, rows, 0);
-    load_pre(pn, u0, rows);
+    load_pre(pn, t0, rows);
   }
   // ---- 3. stage the activation rows in LDS, RMSNorm'd (HF order) when normw is given; rows >= M
   //         are zero so no garbage reaches the sums
@@ -248,12 +260,16 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   }
   __syncthreads();
 
-  // ---- 4. stream the units; each unit's next-unit prefetch is issued before its reduction
-  for (int u = u0; u < n_units; u += nw) {
-    const Pre pc = pn;
-    float acc[NR][MR];
+  // ---- 4. stream the items; each item's next-item prefetch is issued before its reduction.
+  //         Every activation chunk read from LDS feeds all R rows of the item, and each row's
+  //         products are summed in the same order for every G, so G never changes a result.
+  for (int t = t0; t < n_items; t += nw) {
+    Pre pc[G];
 #pragma unroll
-    for (int j = 0; j < NR; j++)
+    for (int g = 0; g < G; g++) pc[g] = pn[g];
+    float acc[R][MR];
+#pragma unroll
+    for (int j = 0; j < R; j++)
 #pragma unroll
       for (int m = 0; m < MR; m++) acc[j][m] = 0.f;
 
@@ -264,119 +280,146 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
       for (int i = 0; i < U; i++) {
         const int c = base + i * 64 + lane;
         if (c < nload) {
-          f16x2 wp[NR][WPL / 2];
 #pragma unroll
-          for (int j = 0; j < NR; j++) {
-            if constexpr (WF == WF_F16) {
+          for (int q = 0; q < XPL; q++) {
+            u32x4 xv[MR];
 #pragma unroll
-              for (int p = 0; p < 4; p++) wp[j][p] = as_h2(wv[j][i][p]);
-            } else {
+            for (int m = 0; m < MR; m++) xv[m] = xs[m * K8 + c * XPL + q];
 #pragma unroll
-              for (int p = 0; p < WPL / 4; p++) i8x4_to_f16(wv[j][i][p], wp[j][2 * p], wp[j][2 * p + 1]);
-            }
-          }
+            for (int j = 0; j < R; j++) {
+              f16x2 w4[4];  // the 8 weights of this row that meet activation chunk q
+              if constexpr (WF == WF_F16) {
 #pragma unroll
-          for (int m = 0; m < MR; m++) {
-#pragma unroll
-            for (int t = 0; t < XPL; t++) {
-              const u32x4 xv = xs[m * K8 + c * XPL + t];
-#pragma unroll
-              for (int p = 0; p < 4; p++) {
-                const f16x2 xp = as_h2(xv[p]);
-#pragma unroll
-                for (int j = 0; j < NR; j++) acc[j][m] = dot2(wp[j][4 * t + p], xp, acc[j][m]);
+                for (int p = 0; p < 4; p++) w4[p] = as_h2(wv[j][i][p]);
+              } else {
+                i8x4_to_f16(wv[j][i][2 * q], w4[0], w4[1]);
+                i8x4_to_f16(wv[j][i][2 * q + 1], w4[2], w4[3]);
               }
+#pragma unroll
+              for (int m = 0; m < MR; m++)
+#pragma unroll
+                for (int p = 0; p < 4; p++) acc[j][m] = dot2(w4[p], as_h2(xv[m][p]), acc[j][m]);
             }
           }
         }
       }
     }
 
-    if (u + nw < n_units) {
-      unit_rows(u + nw, rows);
+    if (t + nw < n_items) {
+      item_rows(t + nw, rows);
       load_step(wv, rows, 0);
-      load_pre(pn, u + nw, rows);
+      load_pre(pn, t + nw, rows);
       have = true;
     }
 
 #pragma unroll
-    for (int j = 0; j < NR; j++)
+    for (int j = 0; j < R; j++)
 #pragma unroll
       for (int m = 0; m < MR; m++) acc[j][m] = wave_sum(acc[j][m]);
 
     if (epi_lane) {
-      float a0 = 0.f, a1 = 0.f;  // this lane's row, selected without dynamic register indexing
 #pragma unroll
-      for (int m = 0; m < MR; m++)
-        if (m == lane) {
-          a0 = acc[0][m];
-          a1 = acc[NR - 1][m];
+      for (int g = 0; g < G; g++) {
+        const int u = t * G + g;
+        if (u >= n_units) break;
+        float a0 = 0.f, a1 = 0.f;  // this lane's row, selected without dynamic register indexing
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+          if (m == lane) {
+            a0 = acc[g * NR][m];
+            a1 = acc[g * NR + NR - 1][m];
+          }
+        if constexpr (WF != WF_F16) {
+          a0 *= (float)pc[g].s0;  // the row scale applied once to the reduced sum (reference kernels.cuh:261)
+          a1 *= (float)pc[g].s1;
         }
-      if constexpr (WF != WF_F16) {
-        a0 *= (float)pc.s0;  // the row scale applied once to the reduced sum (reference kernels.cuh:261)
-        a1 *= (float)pc.s1;
-      }
-      f16* orow = a.out + lane * a.ldo;
-      if constexpr (EPI == 0) {
-        orow[u] = (f16)a0;
-      } else if constexpr (EPI == 1) {
-        orow[u] = pc.r + (f16)a0;  // fp16 add, correctly rounded
-      } else if constexpr (EPI == 2) {
-        orow[u] = silu_mul(a0, a1);
-      } else {
-        const int D = a.D, HD = D >> 1, head = u / HD, d = u - head * HD;
-        const int p = my_pos;
-        const int slot = a.kv_slot >= 0 ? a.kv_slot : a.slot_base + lane;
-        if (a.bias) {
-          a0 += (float)pc.b0;
-          a1 += (float)pc.b1;
+        f16* orow = a.out + lane * a.ldo;
+        if constexpr (EPI == 0) {
+          orow[u] = (f16)a0;
+        } else if constexpr (EPI == 1) {
+          orow[u] = pc[g].r + (f16)a0;  // fp16 add, correctly rounded
+        } else if constexpr (EPI == 2) {
+          orow[u] = silu_mul(a0, a1);
+        } else {
+          const int D = a.D, HD = D >> 1, head = u / HD, d = u - head * HD;
+          const int p = my_pos;
+          const int slot = a.kv_slot >= 0 ? a.kv_slot : a.slot_base + lane;
+          if (a.bias) {
+            a0 += (float)pc[g].b0;
+            a1 += (float)pc[g].b1;
+          }
+          f16 y1 = (f16)a0, y2 = (f16)a1;
+          if (head < a.Hq + a.Hkv) rope_pair(y1, y2, pc[g].cs);
+          f16* dst;
+          if (head < a.Hq) dst = orow + head * D;
+          else if (head < a.Hq + a.Hkv) dst = a.kc + (((int64_t)slot * a.Hkv + head - a.Hq) * a.max_seq + p) * D;
+          else dst = a.vc + (((int64_t)slot * a.Hkv + head - a.Hq - a.Hkv) * a.max_seq + p) * D;
+          dst[d] = y1;
+          dst[d + HD] = y2;
         }
-        f16 y1 = (f16)a0, y2 = (f16)a1;
-        if (head < a.Hq + a.Hkv) rope_pair(y1, y2, pc.cs);
-        f16* dst;
-        if (head < a.Hq) dst = orow + head * D;
-        else if (head < a.Hq + a.Hkv) dst = a.kc + (((int64_t)slot * a.Hkv + head - a.Hq) * a.max_seq + p) * D;
-        else dst = a.vc + (((int64_t)slot * a.Hkv + head - a.Hq - a.Hkv) * a.max_seq + p) * D;
-        dst[d] = y1;
-        dst[d + HD] = y2;
       }
     }
   }
 }
 
 // One launch: the grid fills the resident block slots once, every wave taking the same number
-// of units (within one), so the fused-norm prologue is paid once per block.
-template <int MR, bool NORM, int EPI, int WF>
+// of items (within one), so the fused-norm prologue is paid once per block.
+template <int MR, bool NORM, int EPI, int WF, int G>
 int gemv_launch(const GemvArgs& a, hipStream_t s) {
   const HiDevice* d = hi_device();
   if (!d) return -2;
   const size_t lds = (size_t)MR * a.K * 2;
-  const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MR, NORM, EPI, WF>);
+  const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MR, NORM, EPI, WF, G>);
   const int bpc = hi_blocks_per_cu(fn, kGemvThreads, lds);
   if (bpc < 0) return -2;
   if (bpc == 0) HI_FAIL("gemv: %zu bytes of activation rows do not fit in LDS", lds);
   const int n_units = EPI >= 2 ? a.N / 2 : a.N;
+  const int n_items = (n_units + G - 1) / G;
   const int slots = bpc * d->cus * kGemvWaves;
-  const int per_wave = (n_units + slots - 1) / slots;
-  const int grid = (n_units + kGemvWaves * per_wave - 1) / (kGemvWaves * per_wave);
-  hipLaunchKernelGGL((gemv_kernel<MR, NORM, EPI, WF>), dim3(grid), dim3(kGemvThreads), lds, s, a);
+  const int per_wave = (n_items + slots - 1) / slots;
+  int grid = (n_items + kGemvWaves * per_wave - 1) / (kGemvWaves * per_wave);
+  // An equal split that would leave CUs idle (items just above the resident slots) gives way to
+  // every resident block, the waves taking items in grid stride (counts within one of each other).
+  if (grid < d->cus) {
+    const int all = (n_items + kGemvWaves - 1) / kGemvWaves;
+    grid = all < bpc * d->cus ? all : bpc * d->cus;
+  }
+  hipLaunchKernelGGL((gemv_kernel<MR, NORM, EPI, WF, G>), dim3(grid), dim3(kGemvThreads), lds, s, a);
   HI_TRY(hipGetLastError());
   return 0;
+}
+
+// Units per item. From 4 activation rows on, each 16-byte weight chunk costs M 16-byte activation
+// reads from LDS and M x 4 dot products, and a unit's compute stops overlapping its wave's weight
+// stream; G one-row units per item share every activation read. Measured on MI355X at M = 8
+// (Qwen2.5-1.5B shapes), this pays only for lm_head-sized launches: 2 units per item for fp16
+// weights, 4 for int8. Two-row units (SwiGLU, RoPE) and smaller N ran fastest with one unit per
+// wave, since the extra accumulators cost resident waves. G never changes a result.
+inline int gemv_group(int MR, int epi, int wf, int n_units) {
+  if (MR < 4 || epi >= 2 || wf == WF_I8H || n_units < 32768) return 1;
+  const int G = wf == WF_F16 ? 2 : 4;
+  return G * MR > (MR >= 16 ? 32 : 64) ? G / 2 : G;  // 16 rows also hold 64 registers of activations
 }
 
 // Template selection for one epilogue (each epilogue's instances live in their own file).
 template <int EPI>
 int gemv_run(const GemvArgs& a, int MR, bool norm, int wf, hipStream_t s);
 
-#define HI_GEMV_CASE(mr, nm, wfv) \
-  if (MR == mr && norm == nm && wf == wfv) return gemv_launch<mr, nm, EPI, wfv>(a, s);
-#define HI_GEMV_WF(mr, nm) HI_GEMV_CASE(mr, nm, WF_F16) HI_GEMV_CASE(mr, nm, WF_I8) HI_GEMV_CASE(mr, nm, WF_I8H)
+#define HI_GEMV_CASE(mr, nm, wfv, g) \
+  if (MR == (mr) && norm == (nm) && wf == (wfv) && G == (g)) return gemv_launch<(mr), (nm), EPI, (wfv), (g)>(a, s);
+#define HI_GEMV_WF(mr, nm) HI_GEMV_CASE(mr, nm, WF_F16, 1) HI_GEMV_CASE(mr, nm, WF_I8, 1) HI_GEMV_CASE(mr, nm, WF_I8H, 1)
+#define HI_GEMV_GROUPED(mr, nm) HI_GEMV_CASE(mr, nm, WF_F16, 2) HI_GEMV_CASE(mr, nm, WF_I8, mr >= 16 ? 2 : 4)
 #define HI_GEMV_DEFINE_RUN(EPIV)                                                                  \
   template <>                                                                                     \
   int gemv_run<EPIV>(const GemvArgs& a, int MR, bool norm, int wf, hipStream_t s) {              \
     constexpr int EPI = EPIV;                                                                     \
+    const int G = gemv_group(MR, EPI, wf, EPI >= 2 ? a.N / 2 : a.N);                              \
     HI_GEMV_WF(1, true) HI_GEMV_WF(2, true) HI_GEMV_WF(4, true) HI_GEMV_WF(8, true)               \
     HI_GEMV_WF(1, false) HI_GEMV_WF(2, false) HI_GEMV_WF(4, false) HI_GEMV_WF(8, false)           \
     HI_GEMV_WF(16, false)                                                                         \
-    HI_FAIL("gemv: no kernel for %d rows (norm %d, format %d)", MR, (int)norm, wf);               \
+    if constexpr (EPI <= 1) {                                                                     \
+      HI_GEMV_GROUPED(4, true) HI_GEMV_GROUPED(8, true) HI_GEMV_GROUPED(4, false)                 \
+      HI_GEMV_GROUPED(8, false) HI_GEMV_GROUPED(16, false)                                        \
+    }                                                                                             \
+    HI_FAIL("gemv: no kernel for %d rows (norm %d, format %d, group %d)", MR, (int)norm, wf, G);  \
   }

@@ -249,3 +249,47 @@ def test_full_size_sampled_rows(hi, O):
                 sblk[j], sblk[j + 16] = sh[i], sh[256 + i]
         ref = O.gemv(x, blk, epi=2, normw=nw, scales=sblk)
         check(f"full-size gate/up {'int8' if q else 'fp16'} sampled", got[:, units], ref, 3e-3, 3e-3)
+
+
+@pytest.mark.parametrize("q", [False, True], ids=["fp16", "int8"])
+def test_grouped_units_lm_head_sized(hi, O, q):
+    """From 4 rows on, lm_head-sized launches let one wave stream 2 (fp16) or 4 (int8) output rows
+    at once. N = 32775 leaves a partial last group. Every activation row must stay bit-identical to
+    the 1-row GEMV (one row per wave), for the plain, fused-norm and residual epilogues, and
+    sampled output columns must match the oracle."""
+    import torch
+    r = rng(21)
+    N, K = 32775, 1536
+    g = torch.Generator(device="cuda").manual_seed(21)
+    Wd = (torch.randn(N, K, generator=g, device="cuda") * 0.02).half()
+    sd = None
+    if q:
+        Wd, sd = hi.quantize_rows(Wd)
+    x = h16(r, 16, K)
+    nw = (r.random(K) + 0.5).astype(np.float16)
+    cols = np.concatenate([np.sort(r.choice(N - 8, 120, replace=False)), np.arange(N - 8, N)])
+    Wh = host(Wd[torch.from_numpy(cols).cuda()])
+    sh = None if sd is None else host(sd[torch.from_numpy(cols).cuda()])
+    for norm in [False, True]:
+        nwd = cuda(nw) if norm else None
+        ones = [host(hi.gemv(cuda(x[m:m + 1]), Wd, normw=nwd, scales=sd))[0] for m in range(16)]
+        for M in ([4, 5, 8] if norm else [4, 5, 8, 16]):
+            got = host(hi.gemv(cuda(x[:M]), Wd, normw=nwd, scales=sd))
+            for m in range(M):
+                assert np.array_equal(bits(got[m]), bits(ones[m])), f"norm={norm} M={M} row {m}"
+            ref = O.gemv(x[:M], Wh, normw=nw if norm else None, scales=sh)
+            check(f"grouped {'int8' if q else 'fp16'} norm={norm} M={M} sampled", got[:, cols], ref, 3e-3, 3e-3)
+    # residual epilogue: out = res + x @ W^T, bit-identical per row to the 1-row call
+    res = h16(r, 8, N)
+    ones = []
+    for m in range(8):
+        o = cuda(res[m:m + 1])
+        hi.gemv(cuda(x[m:m + 1]), Wd, out=o, epi=1, scales=sd)
+        ones.append(host(o)[0])
+    o = cuda(res)
+    hi.gemv(cuda(x[:8]), Wd, out=o, epi=1, scales=sd)
+    got = host(o)
+    for m in range(8):
+        assert np.array_equal(bits(got[m]), bits(ones[m])), f"residual row {m}"
+    ref = O.gemv(x[:8], Wh, out=res[:, cols].copy(), epi=1, scales=sh)
+    check(f"grouped {'int8' if q else 'fp16'} residual sampled", got[:, cols], ref, 4e-3, 2e-3)
