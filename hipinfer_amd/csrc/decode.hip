@@ -1,0 +1,354 @@
+// Decode-step kernels around the GEMVs, behind the reference's C-ABI: split-KV decode attention
+// (hi_decode_attn, hi_decode_work_bytes; src/api.cu:643-720, ctypes scripts/hipinfer.py:21-22,30)
+// and the greedy argmax (hi_argmax; api.cu:838-840, kernels.cuh:1883-1931). hi_embed (the
+// reference's internal embed_kernel, kernels.cuh:1876-1881, called from decode_step api.cu:1900)
+// is exported as well so that a caller can assemble a whole decode step from C-ABI calls.
+//
+// Decode attention, one new token per sequence, for gfx950:
+//  * block = (split, kv head, sequence), 4 waves; every block serves all G query heads of its kv
+//    head, so the cache is read once per GQA group. A split covers a contiguous run of keys; the
+//    number of splits in use is derived on the device from pos[b], so a captured graph stays valid
+//    while the context grows;
+//  * a wave takes 64-key tiles: lane l owns key t0 + l, loads its whole K row (D / 8 16-byte loads)
+//    and the tile's V rows are loaded at the same time (neither depends on the other), so a tile
+//    costs one memory round trip. The lane computes its key's logit for every query head in fp32
+//    (q pre-scaled by log2(e) / sqrt(D), the reference's log2-domain softmax, kernels.cuh:1522);
+//  * online softmax per wave (max and sum over the 64 lanes), P.V with each lane owning D / 64
+//    output dims and p read from its key's lane (v_readlane), the 4 waves merged through LDS;
+//  * splits hand their partials (o, m, l) to the last-arriving block of their (sequence, kv head)
+//    with agent-coherent (sc1) stores and loads and a relaxed agent-scope counter, which the last
+//    block resets: no L2 writeback/invalidate fence (gfx950's agent-scope fence costs several
+//    microseconds), and the caller's zeroed work buffer stays zeroed, as the reference requires
+//    (api.cu:648-650).
+#include <type_traits>
+
+#include "hi_common.h"
+
+namespace {
+
+constexpr int kDecodeCounters = 4096;  // as api.cu:651: counters at a fixed offset, then partials
+constexpr int kDecodeMaxSplits = 64;
+constexpr int kDaWaves = 4, kDaTile = 64, kDaBlockKeys = kDaWaves * kDaTile;
+
+__device__ __forceinline__ float ld_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int G, int D>
+__global__ void __launch_bounds__(kDaWaves * 64) decode_attn_kernel(const f16* __restrict__ q, int ldq,
+                                                                    const f16* __restrict__ kc,
+                                                                    const f16* __restrict__ vc, int max_seq, int Hkv,
+                                                                    const int* __restrict__ pos, float* part,
+                                                                    int* counters, int S, f16* __restrict__ out,
+                                                                    int ldo, float scale_log2, int kv_slot) {
+  constexpr int DPL = D / 64;  // output dims per lane
+  constexpr int KC = D / 8;    // 16-byte chunks of a K row
+  __shared__ float qs[G][D];
+  __shared__ float wm[kDaWaves][G], wl[kDaWaves][G];
+  __shared__ float wo[kDaWaves][G][D];
+  __shared__ int is_last;
+  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int Hq = Hkv * G;
+  const int len = min(pos[b] + 1, max_seq);
+  const int S_eff = min(S, (len + kDaBlockKeys - 1) / kDaBlockKeys);
+  if (split >= S_eff) return;
+  const int chunk = (len + S_eff - 1) / S_eff;
+  const int start = split * chunk, end = min(len, start + chunk);
+  const int64_t cb = kv_slot >= 0 ? kv_slot : b;
+  const f16* Kh = kc + (cb * Hkv + hk) * (int64_t)max_seq * D;
+  const f16* Vh = vc + (cb * Hkv + hk) * (int64_t)max_seq * D;
+
+  for (int i = tid; i < G * D; i += kDaWaves * 64) qs[i / D][i % D] = (float)q[(int64_t)b * ldq + hk * G * D + i] * scale_log2;
+  __syncthreads();
+
+  float m[G], l[G], o[G][DPL];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    m[g] = -__builtin_huge_valf();
+    l[g] = 0.f;
+#pragma unroll
+    for (int d = 0; d < DPL; d++) o[g][d] = 0.f;
+  }
+
+  for (int t0 = start + wave * kDaTile; t0 < end; t0 += kDaBlockKeys) {
+    // keeps the q reads from LDS inside the loop: hoisted, G x D of them would sit in registers
+    asm volatile("" ::: "memory");
+    const int n = min(kDaTile, end - t0);
+    const bool valid = lane < n;
+    // K row of this lane's key and the tile's V rows, all issued before any use (rows past the
+    // split's end are clamped to its last key: read, never used)
+    const f16* kr = Kh + (int64_t)(t0 + (valid ? lane : n - 1)) * D;
+    u32x4 kv[KC];
+#pragma unroll
+    for (int c = 0; c < KC; c++) kv[c] = *reinterpret_cast<const u32x4*>(kr + 8 * c);
+    typedef typename std::conditional<DPL == 2, uint32_t, uint16_t>::type VT;
+    VT vv[kDaTile];
+#pragma unroll
+    for (int jj = 0; jj < kDaTile; jj++)
+      vv[jj] = *reinterpret_cast<const VT*>(Vh + (int64_t)(t0 + min(jj, n - 1)) * D + lane * DPL);
+
+    float s[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) s[g] = 0.f;
+#pragma unroll
+    for (int c = 0; c < KC; c++) {
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const f16x2 kh = as_h2(kv[c][p]);
+        const float k0 = (float)kh.x, k1 = (float)kh.y;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+          s[g] = __builtin_fmaf(qs[g][8 * c + 2 * p], k0, s[g]);
+          s[g] = __builtin_fmaf(qs[g][8 * c + 2 * p + 1], k1, s[g]);
+        }
+      }
+    }
+    float p_[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      const float sv = valid ? s[g] : -__builtin_huge_valf();
+      const float mn = fmaxf(m[g], wave_max(sv));  // finite: every tile has a valid key
+      p_[g] = valid ? exp2f(sv - mn) : 0.f;
+      const float a = exp2f(m[g] - mn);  // 0 on the first tile (m = -inf)
+      l[g] = l[g] * a + wave_sum(p_[g]);
+      m[g] = mn;
+#pragma unroll
+      for (int d = 0; d < DPL; d++) o[g][d] *= a;
+    }
+#pragma unroll
+    for (int jj = 0; jj < kDaTile; jj++) {
+      if (jj < n) {  // uniform over the wave
+        float vf[DPL];
+        if constexpr (DPL == 2) {
+          const f16x2 vh = as_h2(vv[jj]);
+          vf[0] = (float)vh.x;
+          vf[1] = (float)vh.y;
+        } else {
+          vf[0] = (float)__builtin_bit_cast(f16, (uint16_t)vv[jj]);
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+          const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p_[g]), jj));
+#pragma unroll
+          for (int d = 0; d < DPL; d++) o[g][d] = __builtin_fmaf(pj, vf[d], o[g][d]);
+        }
+      }
+    }
+  }
+
+  // ---- merge the block's waves (a wave without keys has m = -inf and weight 0)
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    if (lane == 0) {
+      wm[wave][g] = m[g];
+      wl[wave][g] = l[g];
+    }
+#pragma unroll
+    for (int d = 0; d < DPL; d++) wo[wave][g][lane * DPL + d] = o[g][d];
+  }
+  __syncthreads();
+  const bool single = S_eff == 1;
+  float* po = part + (int64_t)kDecodeCounters;  // partials follow the counters (floats)
+  for (int i = tid; i < G * D; i += kDaWaves * 64) {
+    const int g = i / D, d = i % D;
+    float M = -__builtin_huge_valf();
+#pragma unroll
+    for (int w = 0; w < kDaWaves; w++) M = fmaxf(M, wm[w][g]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDaWaves; w++) {
+      const float f = wm[w][g] == -__builtin_huge_valf() ? 0.f : exp2f(wm[w][g] - M);
+      L = __builtin_fmaf(wl[w][g], f, L);
+      O = __builtin_fmaf(wo[w][g][d], f, O);
+    }
+    if (single) {
+      out[(int64_t)b * ldo + (hk * G + g) * D + d] = (f16)(O / L);
+    } else {
+      const int64_t pi = ((int64_t)b * Hq + hk * G + g) * kDecodeMaxSplits + split;
+      st_coherent(po + pi * (D + 2) + d, O);
+      if (d == 0) {
+        st_coherent(po + pi * (D + 2) + D, M);
+        st_coherent(po + pi * (D + 2) + D + 1, L);
+      }
+    }
+  }
+  if (single) return;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are complete
+  __syncthreads();
+  if (tid == 0) {
+    int* ctr = counters + b * Hkv + hk;
+    const int done = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = done == S_eff - 1;
+    if (is_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next launch
+  }
+  __syncthreads();
+  if (!is_last) return;
+  // ---- the last block merges the S_eff splits of every head of its group, in split order
+  for (int i = tid; i < G * D; i += kDaWaves * 64) {
+    const int g = i / D, d = i % D;
+    const float* pp = po + ((int64_t)b * Hq + hk * G + g) * kDecodeMaxSplits * (D + 2);
+    float M = -__builtin_huge_valf();
+    for (int s2 = 0; s2 < S_eff; s2++) M = fmaxf(M, ld_coherent(pp + s2 * (D + 2) + D));
+    float L = 0.f, O = 0.f;
+    for (int s2 = 0; s2 < S_eff; s2++) {
+      const float f = exp2f(ld_coherent(pp + s2 * (D + 2) + D) - M);
+      L = __builtin_fmaf(ld_coherent(pp + s2 * (D + 2) + D + 1), f, L);
+      O = __builtin_fmaf(ld_coherent(pp + s2 * (D + 2) + d), f, O);
+    }
+    out[(int64_t)b * ldo + (hk * G + g) * D + d] = (f16)(O / L);
+  }
+}
+
+// Splits per (sequence, kv head): enough blocks for two per CU (as api.cu:643-646), at most 64;
+// the kernel uses min(S, ceil(len / 256)) of them.
+int decode_splits(int B, int Hkv, int cus) {
+  const int S = (2 * cus + B * Hkv - 1) / (B * Hkv);
+  return S < 1 ? 1 : S > kDecodeMaxSplits ? kDecodeMaxSplits : S;
+}
+
+template <int D>
+int decode_attn_d(int G, dim3 grid, hipStream_t s, const f16* q, int ldq, const f16* kc, const f16* vc, int max_seq,
+                  int Hkv, const int* pos, float* part, int* counters, int S, f16* out, int ldo, float sl2) {
+#define HI_DA(g)                                                                                                      \
+  case g:                                                                                                             \
+    hipLaunchKernelGGL((decode_attn_kernel<g, D>), grid, dim3(kDaWaves * 64), 0, s, q, ldq, kc, vc, max_seq, Hkv, pos, \
+                       part, counters, S, out, ldo, sl2, -1);                                                         \
+    break;
+  switch (G) {
+    HI_DA(1) HI_DA(2) HI_DA(3) HI_DA(4) HI_DA(5) HI_DA(6) HI_DA(7) HI_DA(8)
+    default: HI_FAIL("hi_decode_attn: unsupported GQA group %d (1..8)", G);
+  }
+#undef HI_DA
+  HI_TRY(hipGetLastError());
+  return 0;
+}
+
+// ---- greedy argmax: largest logit, NaN above every number, lowest index on ties; a row of -inf
+//      gives 0 (kernels.cuh:1883-1931)
+__device__ __forceinline__ bool argmax_better(float v, int i, float best, int bi) {
+  const bool vn = v != v, bn = best != best;
+  if (vn != bn) return vn;
+  return (vn || v == best) ? i < bi : v > best;
+}
+
+constexpr int kArgmaxThreads = 1024;
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_kernel(const f16* __restrict__ logits, int V,
+                                                                int* __restrict__ tok_out) {
+  __shared__ float bv[kArgmaxThreads / 64];
+  __shared__ int bi[kArgmaxThreads / 64];
+  const f16* row = logits + (int64_t)blockIdx.x * V;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float best = -__builtin_huge_valf();
+  int idx = 0;
+  if (((uintptr_t)row & 15) == 0) {  // 8 logits per 16-byte load, then the tail
+    const int V8 = V / 8;
+    for (int c = tid; c < V8; c += kArgmaxThreads) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(row + 8 * c);
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const f16x2 h = as_h2(v[p]);
+        if (argmax_better((float)h.x, 8 * c + 2 * p, best, idx)) { best = (float)h.x; idx = 8 * c + 2 * p; }
+        if (argmax_better((float)h.y, 8 * c + 2 * p + 1, best, idx)) { best = (float)h.y; idx = 8 * c + 2 * p + 1; }
+      }
+    }
+    for (int i = 8 * V8 + tid; i < V; i += kArgmaxThreads)
+      if (argmax_better((float)row[i], i, best, idx)) { best = (float)row[i]; idx = i; }
+  } else {
+    for (int i = tid; i < V; i += kArgmaxThreads)
+      if (argmax_better((float)row[i], i, best, idx)) { best = (float)row[i]; idx = i; }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (argmax_better(ov, oi, best, idx)) { best = ov; idx = oi; }
+  }
+  if (lane == 0) {
+    bv[wave] = best;
+    bi[wave] = idx;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgmaxThreads / 64; w++)
+      if (argmax_better(bv[w], bi[w], best, idx)) { best = bv[w]; idx = bi[w]; }
+    tok_out[blockIdx.x] = idx;
+  }
+}
+
+// ---- embedding rows: x[b] = table[tok[b]] (H halves), 16 bytes per thread
+__global__ void __launch_bounds__(256) embed_kernel(const int* __restrict__ tok, const f16* __restrict__ table, int V,
+                                                    int H, f16* __restrict__ x, int64_t ldx) {
+  const int b = blockIdx.x;
+  const int t = tok[b];
+  if (t < 0 || t >= V) return;  // an id outside the vocabulary leaves the row untouched
+  const u32x4* src = reinterpret_cast<const u32x4*>(table + (int64_t)t * H);
+  u32x4* dst = reinterpret_cast<u32x4*>(x + (int64_t)b * ldx);
+  for (int i = threadIdx.x; i < H / 8; i += blockDim.x) dst[i] = src[i];
+}
+
+}  // namespace
+
+// Work bytes for hi_decode_attn (as api.cu:651-655): 4096 int counters the caller zeroes once (the
+// kernel leaves them zeroed), then B * Hq * 64 * (D + 2) fp32 partials.
+HI_EXPORT size_t hi_decode_work_bytes(int B, int Hq, int Hkv, int D) {
+  (void)Hkv;
+  return (size_t)kDecodeCounters * 4 + (size_t)(B > 0 ? B : 0) * (Hq > 0 ? Hq : 0) * kDecodeMaxSplits * (D + 2) * 4;
+}
+
+// out[b, h*D : (h+1)*D] = softmax(q_h . K[0..pos[b]] / sqrt(D)) V for every query head h of
+// sequence b, K/V read from cache slot b ([slots][Hkv][max_seq][D] fp16), the kv head of h being
+// h / (Hq / Hkv). work: hi_decode_work_bytes(B, Hq, Hkv, D) bytes, zeroed once by the caller.
+HI_EXPORT int hi_decode_attn(const void* q, int ldq, const void* kc, const void* vc, int max_seq, const int* pos,
+                             void* out, int ldo, int B, int Hq, int Hkv, int D, void* work, void* s) {
+  const HiDevice* d = hi_device();
+  if (!d) return -2;
+  if (D != 64 && D != 128) HI_FAIL("hi_decode_attn: head dim %d (64 or 128)", D);
+  if (B < 0 || Hkv < 1 || Hq < Hkv || Hq % Hkv || Hq / Hkv > 8 || max_seq < 1)
+    HI_FAIL("hi_decode_attn: B %d, Hq %d, Hkv %d (Hq / Hkv in 1..8), max_seq %d", B, Hq, Hkv, max_seq);
+  if (B == 0) return 0;
+  if (B * Hkv > kDecodeCounters) HI_FAIL("hi_decode_attn: B*Hkv %d > %d", B * Hkv, kDecodeCounters);
+  if (!q || !kc || !vc || !pos || !out || !work) HI_FAIL("hi_decode_attn: null pointer");
+  if (((uintptr_t)q & 1) || ((uintptr_t)kc & 15) || ((uintptr_t)vc & 15) || ((uintptr_t)work & 3) || (((uintptr_t)out) & 1))
+    HI_FAIL("hi_decode_attn: kc and vc must be 16-byte aligned");
+  if (ldq < Hq * D || ldo < Hq * D) HI_FAIL("hi_decode_attn: ldq %d / ldo %d < Hq * D = %d", ldq, ldo, Hq * D);
+  const int S = decode_splits(B, Hkv, d->cus);
+  const float sl2 = 1.4426950408889634f / sqrtf((float)D);
+  const dim3 grid(S, Hkv, B);
+  int* counters = (int*)work;
+  float* part = (float*)work;
+  const hipStream_t st = (hipStream_t)s;
+  if (D == 64)
+    return decode_attn_d<64>(Hq / Hkv, grid, st, (const f16*)q, ldq, (const f16*)kc, (const f16*)vc, max_seq, Hkv, pos,
+                             part, counters, S, (f16*)out, ldo, sl2);
+  return decode_attn_d<128>(Hq / Hkv, grid, st, (const f16*)q, ldq, (const f16*)kc, (const f16*)vc, max_seq, Hkv, pos,
+                            part, counters, S, (f16*)out, ldo, sl2);
+}
+
+// tok_out[b] = argmax of logits[b, 0:V] (fp16): NaN ranks above every number, ties go to the
+// lowest index, an all -inf row gives 0 (api.cu:838-840).
+HI_EXPORT int hi_argmax(const void* logits, int B, int V, int* tok_out, void* s) {
+  if (!hi_device()) return -2;
+  if (B < 0 || V < 1) HI_FAIL("hi_argmax: B %d, V %d", B, V);
+  if (B == 0) return 0;
+  if (!logits || !tok_out || ((uintptr_t)logits & 1)) HI_FAIL("hi_argmax: null or misaligned pointer");
+  hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(kArgmaxThreads), 0, (hipStream_t)s, (const f16*)logits, V, tok_out);
+  HI_TRY(hipGetLastError());
+  return 0;
+}
+
+// x[b, 0:H] = table[tok[b], 0:H] for b < B (no reference export: the reference's engine runs its
+// embed_kernel internally). Token ids outside [0, V) leave the row untouched.
+HI_EXPORT int hi_embed(const int* tok, const void* table, int V, int H, void* x, int ldx, int B, void* s) {
+  if (!hi_device()) return -2;
+  if (B < 0 || V < 1 || H < 8 || H % 8 || ldx % 8 || ldx < H) HI_FAIL("hi_embed: B %d V %d H %d ldx %d", B, V, H, ldx);
+  if (B == 0) return 0;
+  if (!tok || !table || !x || ((uintptr_t)table & 15) || ((uintptr_t)x & 15))
+    HI_FAIL("hi_embed: null pointer or table / x not 16-byte aligned");
+  hipLaunchKernelGGL(embed_kernel, dim3(B), dim3(256), 0, (hipStream_t)s, tok, (const f16*)table, V, H, (f16*)x,
+                     (int64_t)ldx);
+  HI_TRY(hipGetLastError());
+  return 0;
+}

@@ -42,13 +42,18 @@ _OPTIONAL = {
     "hi_moe_router": [P, I, P, I, I, I, I, I, P, P, P],
     "hi_moe_work_bytes": [I, I, I, I, I],
     "hi_moe_experts": [P, I, P, P, P, P, I, I, I, I, I, I, F, P, I, I, P, P],
+    "hi_decode_work_bytes": [I, I, I, I],
+    "hi_decode_attn": [P, I, P, P, I, P, P, I, I, I, I, I, P, P],
+    "hi_argmax": [P, I, I, P, P],
+    "hi_embed": [P, P, I, I, P, I, I, P],
 }
 for _name, _args in list(_SIGS.items()) + [(n, a) for n, a in _OPTIONAL.items() if hasattr(lib, n)]:
     _fn = getattr(lib, _name)
     _fn.argtypes = _args
     _fn.restype = I
-if hasattr(lib, "hi_moe_work_bytes"):
-    lib.hi_moe_work_bytes.restype = C.c_size_t
+for _name in ("hi_moe_work_bytes", "hi_decode_work_bytes"):
+    if hasattr(lib, _name):
+        getattr(lib, _name).restype = C.c_size_t
 MOE_NORM_TOPK, MOE_FP16_WEIGHTS = 1, 2  # moe_flags bits (reference scripts/hipinfer.py:67)
 
 
@@ -158,6 +163,45 @@ def moe_experts(xn, wgu, wdown, idx, w, x, flags, scale=1.0, path=0):
 
 
 # ------------------------------------------------------------------ int8 weight format (GPU)
+def decode_attn(q, kc, vc, pos, Hq, Hkv, out=None, work=None):
+    """Decode attention (reference scripts/hipinfer.py:180-190): q [B, ldq]; kc/vc [B, Hkv, max_seq, D]
+    fp16; pos [B] int32 (query b attends to keys 0..pos[b] of cache slot b). work: zeroed once,
+    hi_decode_work_bytes(B, Hq, Hkv, D) bytes (the kernel leaves its counters zeroed)."""
+    B = q.shape[0]
+    D = kc.shape[-1]
+    if out is None:
+        out = torch.empty(B, Hq * D, dtype=torch.float16, device=q.device)
+    if work is None:
+        work = torch.zeros(lib.hi_decode_work_bytes(B, Hq, Hkv, D), dtype=torch.uint8, device=q.device)
+    _dev(q, kc, vc, pos, out, work)
+    _ok(lib.hi_decode_attn(_p(q), q.stride(0), _p(kc), _p(vc), kc.shape[2], _p(pos), _p(out), out.stride(0), B, Hq, Hkv, D,
+                           _p(work), _s()), "decode_attn")
+    return out
+
+
+def argmax(logits, out=None):
+    """Greedy token per row of logits [B, V] fp16 (reference hi_argmax, api.cu:838): NaN ranks
+    highest, ties go to the lowest index, an all -inf row gives 0."""
+    B, V = logits.shape
+    logits = logits.contiguous()
+    if out is None:
+        out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    _dev(logits, out)
+    _ok(lib.hi_argmax(_p(logits), B, V, _p(out), _s()), "argmax")
+    return out
+
+
+def embed(tok, table, out=None):
+    """Embedding rows out[b] = table[tok[b]] (the reference engine's embed_kernel)."""
+    B = tok.shape[0]
+    V, H = table.shape
+    if out is None:
+        out = torch.empty(B, H, dtype=table.dtype, device=table.device)
+    _dev(tok, table, out)
+    _ok(lib.hi_embed(_p(tok), _p(table), V, H, _p(out), out.stride(0), B, _s()), "embed")
+    return out
+
+
 def quantize_rows(w):
     """scripts/export.py:54-68 on the GPU, bit-exact: s[n] = fp16(max_k |w[n, k]| / 127),
     q = clamp(round(w / s), -127, 127), q = 0 for an all-zero row. Returns (q int8, s fp16)."""

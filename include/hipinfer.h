@@ -82,6 +82,26 @@ int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const void* wdown,
                    int E, int k, int H, int I, int flags, float scale, void* x, int ldx, int path, void* work,
                    void* stream);
 
+/* ---- decode-step kernels around the GEMVs
+ * Bytes of the workspace hi_decode_attn needs: 4096 int counters (zeroed once by the caller, left
+ * zeroed by every launch), then B * Hq * 64 * (D + 2) fp32 split partials. Replaces api.cu:651-656
+ * (hi_decode_work_bytes); hipinfer.py:21-22. */
+size_t hi_decode_work_bytes(int B, int Hq, int Hkv, int D);
+/* Decode attention of B new tokens: out[b, h*D:(h+1)*D] = softmax(q_h . K_slot_b[0..pos[b]] / sqrt(D)) V,
+ * caches kc / vc [slots][Hkv][max_seq][D] fp16, query head h reading kv head h / (Hq / Hkv); D 64 or 128,
+ * Hq / Hkv in 1..8, B * Hkv <= 4096. Split over the keys on the device (graph-capturable while pos grows).
+ * Replaces api.cu:715-720 (hi_decode_attn); hipinfer.py:30. */
+int hi_decode_attn(const void* q, int ldq, const void* kc, const void* vc, int max_seq, const int* pos, void* out,
+                   int ldo, int B, int Hq, int Hkv, int D, void* work, void* stream);
+/* Greedy token of each row of logits [B, V] fp16: the largest value, NaN above every number, the lowest
+ * index on ties, 0 for a row of -inf. Replaces api.cu:838-840 (hi_argmax); kernels.cuh:1883-1931. */
+int hi_argmax(const void* logits, int B, int V, int* tok_out, void* stream);
+/* Embedding rows x[b, 0:H] = table[tok[b], 0:H] (table [V, H] fp16, H % 8 == 0); ids outside [0, V)
+ * leave the row untouched. No reference export: the reference's engine runs the same gather
+ * (embed_kernel, kernels.cuh:1876-1881) inside decode_step (api.cu:1900); exported here so that a
+ * caller can build the whole decode step from C-ABI calls. */
+int hi_embed(const int* tok, const void* table, int V, int H, void* x, int ldx, int B, void* stream);
+
 /* ---- RMSNorm (unfused form of the GEMV prologue; the reference's tests build references with it)
  * y[M, H] = w * fp16(x * rsqrt(mean(x^2) + eps)), rows contiguous. Replaces api.cu:76-79
  * (hi_rmsnorm); hipinfer.py:13. */

@@ -19,6 +19,9 @@
  *                       int8 = fp32 math on fp16(q*s), tests/test_kernels.py:447
  *   or_moe_router       src/kernels.cuh:2091-2147, argmax_better 1886-1890, docs/moe-design.md:186-201
  *   or_moe_experts      src/kernels.cuh:2156-2209 and 2250-2276, scripts/ref_engine.py:60-73
+ *   or_decode_attn      src/kernels.cuh:1486-1660 (decode_attn_kernel), api.cu:694-720;
+ *                       CPU reference form tests/test_kernels.py:298-307 (ref_attn)
+ *   or_argmax           src/kernels.cuh:1883-1931 (argmax_better, block_argmax, argmax_kernel)
  *
  * fp16 conversions are this file's own IEEE binary16 routines (round to nearest even, subnormals,
  * overflow to inf). Accumulation is fp64; the reference accumulates in fp32 in kernel-specific
@@ -401,6 +404,65 @@ int or_moe_experts(const uint16_t* xn, int64_t ldxn, const uint16_t* wgu, const 
     }
     free(act);
     free(sum);
+  }
+  return 0;
+}
+
+/* Decode attention (the reference's decode_attn_kernel, src/kernels.cuh:1486-1660, host
+ * api.cu:694-720; CPU reference form tests/test_kernels.py:298-307 ref_attn): for query head h of
+ * sequence b, kv head h / (Hq / Hkv), keys and values 0..pos[b] of cache slot b:
+ * out = fp16(sum_j softmax_j(q . k_j / sqrt(D)) v_j), in fp64 (an upper bound on the reference's
+ * fp32 log2-domain online softmax). */
+int or_decode_attn(const uint16_t* q, int64_t ldq, const uint16_t* kc, const uint16_t* vc, int max_seq,
+                   const int32_t* pos, uint16_t* out, int64_t ldo, int B, int Hq, int Hkv, int D) {
+  if (B < 0 || Hkv < 1 || Hq < Hkv || Hq % Hkv || D < 1 || max_seq < 1) return -1;
+  for (int b = 0; b < B; b++)
+    if (pos[b] < 0 || pos[b] >= max_seq) return -1;
+  const int G = Hq / Hkv;
+#pragma omp parallel for schedule(static)
+  for (int bh = 0; bh < B * Hq; bh++) {
+    const int b = bh / Hq, h = bh % Hq, hk = h / G, L = pos[b] + 1;
+    const uint16_t* qh = q + (int64_t)b * ldq + (int64_t)h * D;
+    const uint16_t* K = kc + ((int64_t)b * Hkv + hk) * max_seq * D;
+    const uint16_t* V = vc + ((int64_t)b * Hkv + hk) * max_seq * D;
+    double* s = (double*)malloc((size_t)L * sizeof(double));
+    double mx = -INFINITY;
+    for (int j = 0; j < L; j++) {
+      double acc = 0.0;
+      for (int d = 0; d < D; d++) acc += (double)or_h2f(qh[d]) * (double)or_h2f(K[(int64_t)j * D + d]);
+      s[j] = acc / sqrt((double)D);
+      if (s[j] > mx) mx = s[j];
+    }
+    double den = 0.0;
+    for (int j = 0; j < L; j++) {
+      s[j] = exp(s[j] - mx);
+      den += s[j];
+    }
+    for (int d = 0; d < D; d++) {
+      double o = 0.0;
+      for (int j = 0; j < L; j++) o += s[j] * (double)or_h2f(V[(int64_t)j * D + d]);
+      out[(int64_t)b * ldo + (int64_t)h * D + d] = or_f2h((float)(o / den));
+    }
+    free(s);
+  }
+  return 0;
+}
+
+/* Greedy token of each row (src/kernels.cuh:1883-1931): the largest logit, NaN above every number,
+ * the lowest index on ties, starting from (-inf, 0) so a row of -inf gives 0. */
+int or_argmax(const uint16_t* logits, int B, int V, int32_t* tok) {
+  if (B < 0 || V < 1) return -1;
+  for (int b = 0; b < B; b++) {
+    float best = -INFINITY;
+    int bi = 0;
+    for (int i = 0; i < V; i++) {
+      const float v = or_h2f(logits[(int64_t)b * V + i]);
+      if (argmax_better(v, i, best, bi)) {
+        best = v;
+        bi = i;
+      }
+    }
+    tok[b] = bi;
   }
   return 0;
 }

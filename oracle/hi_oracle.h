@@ -48,6 +48,10 @@ int or_moe_experts(const uint16_t* xn, int64_t ldxn, const uint16_t* wgu, const 
                    const float* w, int M, int E, int k, int H, int I, int flags, float scale, uint16_t* x,
                    int64_t ldx);
 
+int or_decode_attn(const uint16_t* q, int64_t ldq, const uint16_t* kc, const uint16_t* vc, int max_seq,
+                   const int32_t* pos, uint16_t* out, int64_t ldo, int B, int Hq, int Hkv, int D);
+int or_argmax(const uint16_t* logits, int B, int V, int32_t* tok);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,8 @@ def _load():
         "or_gemm": ([P, I64, P, P, P, P, I64, I, I, I, I], I),
         "or_moe_router": ([P, I64, P, I, I, I, I, I, P, P], I),
         "or_moe_experts": ([P, I64, P, P, P, P, I, I, I, I, I, I, F, P, I64], I),
+        "or_decode_attn": ([P, I64, P, P, I, P, P, I64, I, I, I, I], I),
+        "or_argmax": ([P, I, I, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -217,3 +219,23 @@ def moe_experts(xn, wgu, wdown, idx, w, x, flags, scale=1.0):
     _ok(lib.or_moe_experts(_p(xn), H, _p(wgu), _p(wdown), _p(idx), _p(w), M, E, k, H, I2 // 2, flags, scale, _p(x), H),
         "moe_experts")
     return x
+
+
+def decode_attn(q, kc, vc, pos, Hq, Hkv):
+    """Decode attention (src/kernels.cuh:1486-1660; tests/test_kernels.py:298-307): q [B, Hq*D];
+    kc/vc [B, Hkv, max_seq, D]; query b attends to keys 0..pos[b] of slot b. Returns [B, Hq*D] fp16."""
+    q, kc, vc, pos = _c(q, np.float16), _c(kc, np.float16), _c(vc, np.float16), _c(pos, np.int32)
+    B, Hkv_, S, D = kc.shape
+    assert Hkv_ == Hkv
+    out = np.empty((B, Hq * D), np.float16)
+    _ok(lib.or_decode_attn(_p(q), q.shape[1], _p(kc), _p(vc), S, _p(pos), _p(out), Hq * D, B, Hq, Hkv, D), "decode_attn")
+    return out
+
+
+def argmax(logits):
+    """Greedy token per row (src/kernels.cuh:1883-1931): NaN highest, lowest index on ties, 0 for -inf rows."""
+    logits = _c(logits, np.float16)
+    B, V = logits.shape
+    tok = np.empty(B, np.int32)
+    _ok(lib.or_argmax(_p(logits), B, V, _p(tok)), "argmax")
+    return tok

@@ -340,3 +340,79 @@ def test_moe_experts_vs_dense_float64():
             act = gg / (1 + np.exp(-gg)) * uu
             ref[t] += w[t, j] * (act @ wdn[e].astype(np.float64).T)
     assert np.allclose(x.astype(np.float64), ref, rtol=1e-2, atol=1e-2)
+
+
+def _np_decode_attn(q, kc, vc, pos, Hq, Hkv):
+    """Independent float64 restatement (numpy, the reference's ref_attn form, tests/test_kernels.py:298-307)."""
+    B, _, S, D = kc.shape
+    G = Hq // Hkv
+    out = np.empty((B, Hq * D))
+    for b in range(B):
+        L = pos[b] + 1
+        qb = q[b].astype(np.float64).reshape(Hq, D)
+        k = np.repeat(kc[b, :, :L].astype(np.float64), G, axis=0)  # [Hq, L, D]
+        v = np.repeat(vc[b, :, :L].astype(np.float64), G, axis=0)
+        s = np.einsum("hd,hld->hl", qb, k) / np.sqrt(D)
+        p = np.exp(s - s.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        out[b] = np.einsum("hl,hld->hd", p, v).reshape(-1)
+    return out
+
+
+def test_decode_attn_closed_forms():
+    """One key: the output is that key's value row (softmax of one logit is 1). Identical keys or a
+    zero query: uniform weights, the mean of the values. The kv head of query head h is h / G."""
+    r = np.random.default_rng(30)
+    B, Hkv, G, S, D = 2, 3, 2, 40, 64
+    Hq = Hkv * G
+    kc = (r.standard_normal((B, Hkv, S, D))).astype(np.float16)
+    vc = (r.standard_normal((B, Hkv, S, D))).astype(np.float16)
+    q = r.standard_normal((B, Hq * D)).astype(np.float16)
+    out = O.decode_attn(q, kc, vc, np.zeros(B, np.int32), Hq, Hkv)
+    for b in range(B):
+        for h in range(Hq):
+            assert np.array_equal(out[b, h * D:(h + 1) * D], vc[b, h // G, 0]), (b, h)
+    pos = np.array([17, 39], np.int32)
+    out = O.decode_attn(np.zeros_like(q), kc, vc, pos, Hq, Hkv)
+    for b in range(B):
+        for h in range(Hq):
+            mean = vc[b, h // G, :pos[b] + 1].astype(np.float64).mean(0)
+            assert np.array_equal(out[b, h * D:(h + 1) * D], mean.astype(np.float32).astype(np.float16)), (b, h)
+    kc2 = np.repeat(kc[:, :, :1], S, axis=2)
+    out = O.decode_attn(q, kc2, vc, pos, Hq, Hkv)
+    out0 = O.decode_attn(np.zeros_like(q), kc, vc, pos, Hq, Hkv)
+    assert np.array_equal(out, out0)
+
+
+def test_decode_attn_vs_numpy_float64():
+    r = np.random.default_rng(31)
+    for B, Hkv, G, S, D in [(3, 2, 4, 300, 128), (2, 4, 1, 100, 64), (1, 1, 7, 513, 128)]:
+        Hq = Hkv * G
+        kc = r.standard_normal((B, Hkv, S, D)).astype(np.float16)
+        vc = r.standard_normal((B, Hkv, S, D)).astype(np.float16)
+        q = r.standard_normal((B, Hq * D)).astype(np.float16)
+        pos = r.integers(0, S, B).astype(np.int32)
+        got = O.decode_attn(q, kc, vc, pos, Hq, Hkv).astype(np.float64)
+        ref = _np_decode_attn(q, kc, vc, pos, Hq, Hkv)
+        # fp16 rounding of a float64 value: half an ulp of fp16 (2^-11 relative), plus the tiny
+        # difference in summation order
+        assert np.all(np.abs(got - ref) <= 2.0 ** -11 * np.abs(ref) + 1e-7), (B, Hkv, G, S, D)
+
+
+def test_argmax_matches_numpy_and_edge_rows():
+    """The reference's argmax cases (tests/test_kernels.py:208-221): ties to the lowest index, NaN
+    wins, a row of -inf or of NaN gives 0, +inf; numpy's argmax has the same rules."""
+    r = np.random.default_rng(32)
+    V = 32000
+    lg = r.standard_normal((8, V)).astype(np.float16)
+    lg[1, 100] = lg[1, 31999] = 20.0
+    lg[2, 5000] = np.nan
+    lg[2, 7] = np.nan
+    lg[3] = -np.inf
+    lg[4] = np.nan
+    lg[5, 31999] = np.inf
+    lg[6, 17] = lg[6, 12] = lg[6, 30000] = 60000.0
+    lg[7] = 0.0
+    got = O.argmax(lg)
+    assert np.array_equal(got, np.argmax(lg, -1).astype(np.int32)), got
+    assert list(got[[1, 3, 4, 6, 7]]) == [100, 0, 0, 12, 0]
