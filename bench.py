@@ -182,6 +182,67 @@ class PrefillModel:
                 hi.gemm(b["act"], W, out=b["x"], epi=1, scales=s)
 
 
+def decode_step_bench(torch, hi, model, steps, ctxs=(1024, 4096)):
+    """The whole greedy decode step of Llama-3.1-8B at batch 1 (hipinfer_amd.engine.DecodeStep:
+    embed, 32 x [QKV+RoPE+KV write, decode attention, o + residual, gate/up + SwiGLU, down +
+    residual], lm_head, argmax; the reference's decode_step, api.cu:1891-1952) over a KV cache
+    already holding ctx positions, captured once as a hipGraph and replayed; plus the 32 layers'
+    decode attention alone at each context (the kernel's HBM roofline: every cached K and V byte of
+    the context is read once per layer)."""
+    from hipinfer_amd.engine import DecodeStep
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEED + 20)
+    embed = torch.empty(V, H, dtype=torch.float16, device="cuda").normal_(0.0, 1.0, generator=g)
+    cfg = dict(H=H, Hq=HQ, Hkv=HKV, D=D, I=I, V=V, L=L, eps=1e-5, theta=500000.0)
+    max_seq = max(ctxs) + 2 * steps + 16
+    res = {"config": "Llama-3.1-8B greedy decode step, batch 1, KV cache of ctx positions (synthetic), hipGraph replay"}
+    for q8 in ([False, True] if model.q8 is not None else [False]):
+        layers = []
+        for l in range(L):
+            ly = {k: (model.layers[l][k] if not q8 else model.q8[l][k]) for k in SHAPES}
+            ly.update(n1=model.layers[l]["n1"], n2=model.layers[l]["n2"], bqkv=None)
+            layers.append(ly)
+        W = {"embed": embed, "lm": model.lm if not q8 else model.lm_q, "nf": model.nf, "layers": layers}
+        ds = DecodeStep(cfg, W, 1, max_seq)
+        for k in ds.kc + ds.vc:
+            k.normal_(0.0, 1.0, generator=g)
+        ds.pos.fill_(min(ctxs) - 1)
+        ds.step()  # eager first step: kernel attributes and occupancy queries happen outside capture
+        torch.cuda.synchronize()
+        gr = ds.capture()
+        for ctx in ctxs:
+            ds.pos.fill_(ctx - 1)
+            ds.tok.fill_(1)
+            ms, _ = time_graph(torch, gr, steps, 2)
+            kv = L * HKV * (ctx + 2 + steps // 2) * D * 2 * 2  # K and V bytes read per token (mean context)
+            wb = weight_bytes(q8) + H * 2  # + the embedding row
+            gbs = (wb + kv) / (ms * 1e-3) / 1e9
+            res[f"ctx{ctx}_{'int8' if q8 else 'fp16'}"] = {
+                "ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
+                "bytes_per_token": wb + kv, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}
+        if not q8:
+            # decode attention alone, the 32 layers back to back
+            for ctx in ctxs:
+                ds.pos.fill_(ctx - 1)
+
+                def attn():
+                    for l in range(L):
+                        hi.decode_attn(ds.q, ds.kc[l], ds.vc[l], ds.pos, HQ, HKV, out=ds.att, work=ds.work)
+                ga = capture(torch, attn)
+                ms, _ = time_graph(torch, ga, steps, 2)
+                us = ms * 1e3 / L
+                b = HKV * ctx * D * 2 * 2 + HQ * D * 2 * 2
+                res[f"attention_ctx{ctx}"] = {"us_per_layer": round(us, 2), "bytes_per_layer": b,
+                                             "GB/s": round(b / us / 1e3, 1),
+                                             "pct_hbm_peak": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 1)}
+                del ga
+        del gr, ds
+        torch.cuda.empty_cache()
+    del embed
+    torch.cuda.empty_cache()
+    return res
+
+
 def prefill_bench(torch, hi, steps, warmup, q8_too):
     """Per-layer time and TFLOP/s of the four prefill GEMMs at M in {128, 512, 1024}, and of each
     GEMM kind alone at M = 1024 (the kernel the MFMA roofline is quoted on)."""
@@ -425,6 +486,7 @@ def main():
     ap.add_argument("--no-int8", action="store_true")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM (C3) section")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C4 / C5 sections")
+    ap.add_argument("--no-step", action="store_true", help="skip the whole decode step (with attention) section")
     ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe"] +
                     [k + q for k in ("qkv", "o", "gate_up", "down", "lm_head") for q in ("", "8")], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
@@ -526,6 +588,9 @@ def main():
     roofline["traffic"] = traffic_from_profile()
     roofline["traffic_source"] = "profiles/gemv_gate_up_llama31_8b_hbm_bytes.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)"
     res["roofline"] = roofline
+    if not args.no_step:
+        log("decode step ...")
+        res["decode_step"] = decode_step_bench(torch, hi, model, args.steps)
     if not args.no_gemm:
         log("prefill GEMM ...")
         res["prefill_gemm"] = prefill_bench(torch, hi, args.steps, args.warmup, not args.no_int8)

@@ -24,11 +24,16 @@
 
 #include "hi_common.h"
 
+#ifndef HI_DA_WAVES
+#define HI_DA_WAVES 4
+#endif
+
 namespace {
 
 constexpr int kDecodeCounters = 4096;  // as api.cu:651: counters at a fixed offset, then partials
 constexpr int kDecodeMaxSplits = 64;
-constexpr int kDaWaves = 4, kDaTile = 64, kDaBlockKeys = kDaWaves * kDaTile;
+constexpr int kDaTile = 64;  // keys per wave tile (one per lane)
+constexpr int kDaWaves = HI_DA_WAVES;  // waves per block
 
 __device__ __forceinline__ float ld_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -37,32 +42,58 @@ __device__ __forceinline__ void st_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int G, int D>
-__global__ void __launch_bounds__(kDaWaves * 64) decode_attn_kernel(const f16* __restrict__ q, int ldq,
-                                                                    const f16* __restrict__ kc,
-                                                                    const f16* __restrict__ vc, int max_seq, int Hkv,
-                                                                    const int* __restrict__ pos, float* part,
-                                                                    int* counters, int S, f16* __restrict__ out,
-                                                                    int ldo, float scale_log2, int kv_slot) {
-  constexpr int DPL = D / 64;  // output dims per lane
-  constexpr int KC = D / 8;    // 16-byte chunks of a K row
-  __shared__ float qs[G][D];
-  __shared__ float wm[kDaWaves][G], wl[kDaWaves][G];
-  __shared__ float wo[kDaWaves][G][D];
+// LDS of one block: the waves' K tiles and softmax weights while the keys stream, then (after a
+// barrier) the waves' partial results and the split merge's tables in the same bytes.
+template <int G, int D, int NWV>
+struct DaSmem {
+  static constexpr int CPR = D / 8;
+  struct Loop {
+    u32x4 ks[NWV][kDaTile * CPR];      // K tile, chunk c of row r at slot c ^ (r % CPR)
+    uint32_t ps[NWV][G][kDaTile / 2];  // softmax weights, fp16 pairs of keys
+  };
+  struct Merge {
+    float wo[NWV][G][D];
+    float sm[G][kDecodeMaxSplits], sw[G][kDecodeMaxSplits];
+  };
+  union {
+    Loop loop;
+    Merge merge;
+  };
+};
+
+template <int G, int D, int NWV>
+__global__ void __launch_bounds__(NWV * 64) decode_attn_kernel(const f16* __restrict__ q, int ldq,
+                                                               const f16* __restrict__ kc, const f16* __restrict__ vc,
+                                                               int max_seq, int Hkv, const int* __restrict__ pos,
+                                                               float* part, int* counters, int S, f16* __restrict__ out,
+                                                               int ldo, float scale_log2, int kv_slot) {
+  constexpr int DPL = D / 64;        // output dims per lane
+  constexpr int CPR = D / 8;         // 16-byte chunks of a K row
+  constexpr int RPI = 64 / CPR;      // K rows per 1 KB DMA instruction
+  constexpr int BK = NWV * kDaTile;  // keys per block pass
+  constexpr int NT = NWV * 64;
+  __shared__ DaSmem<G, D, NWV> sh;
+  __shared__ u32x4 qs[G][D / 8];  // the G query rows, fp16
+  __shared__ float wm[NWV][G], wl[NWV][G];
   __shared__ int is_last;
   const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int Hq = Hkv * G;
   const int len = min(pos[b] + 1, max_seq);
-  const int S_eff = min(S, (len + kDaBlockKeys - 1) / kDaBlockKeys);
+  const int S_eff = min(S, (len + BK - 1) / BK);
   if (split >= S_eff) return;
   const int chunk = (len + S_eff - 1) / S_eff;
   const int start = split * chunk, end = min(len, start + chunk);
   const int64_t cb = kv_slot >= 0 ? kv_slot : b;
   const f16* Kh = kc + (cb * Hkv + hk) * (int64_t)max_seq * D;
   const f16* Vh = vc + (cb * Hkv + hk) * (int64_t)max_seq * D;
+  const __amdgpu_buffer_rsrc_t k_rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(Kh), (short)0, end * D * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(Vh), (short)0, end * D * 2, 0x00020000);
 
-  for (int i = tid; i < G * D; i += kDaWaves * 64) qs[i / D][i % D] = (float)q[(int64_t)b * ldq + hk * G * D + i] * scale_log2;
+  for (int i = tid; i < G * D / 8; i += NT)
+    qs[i / (D / 8)][i % (D / 8)] = *reinterpret_cast<const u32x4*>(q + (int64_t)b * ldq + hk * G * D + 8 * i);
   __syncthreads();
 
   float m[G], l[G], o[G][DPL];
@@ -74,39 +105,50 @@ __global__ void __launch_bounds__(kDaWaves * 64) decode_attn_kernel(const f16* _
     for (int d = 0; d < DPL; d++) o[g][d] = 0.f;
   }
 
-  for (int t0 = start + wave * kDaTile; t0 < end; t0 += kDaBlockKeys) {
-    // keeps the q reads from LDS inside the loop: hoisted, G x D of them would sit in registers
+  for (int t0 = start + wave * kDaTile; t0 < end; t0 += BK) {
+    // keeps the q reads from LDS inside the loop: hoisted, they would sit in registers
     asm volatile("" ::: "memory");
     const int n = min(kDaTile, end - t0);
     const bool valid = lane < n;
-    // K row of this lane's key and the tile's V rows, all issued before any use (rows past the
-    // split's end are clamped to its last key: read, never used)
-    const f16* kr = Kh + (int64_t)(t0 + (valid ? lane : n - 1)) * D;
-    u32x4 kv[KC];
-#pragma unroll
-    for (int c = 0; c < KC; c++) kv[c] = *reinterpret_cast<const u32x4*>(kr + 8 * c);
+    // the tile's V rows (lane l: dims l*DPL..) and its K rows (1 KB per instruction, straight into
+    // LDS, swizzled so that the one-key-per-lane reads below are conflict-free), all in flight at
+    // once; rows at or past the split's end read as zeros through the buffer bounds
     typedef typename std::conditional<DPL == 2, uint32_t, uint16_t>::type VT;
     VT vv[kDaTile];
 #pragma unroll
-    for (int jj = 0; jj < kDaTile; jj++)
-      vv[jj] = *reinterpret_cast<const VT*>(Vh + (int64_t)(t0 + min(jj, n - 1)) * D + lane * DPL);
+    for (int jj = 0; jj < kDaTile; jj++) {
+      const int off = ((t0 + jj) * D + lane * DPL) * 2;
+      if constexpr (DPL == 2) vv[jj] = __builtin_amdgcn_raw_buffer_load_b32(v_rs, off, 0, 0);
+      else vv[jj] = __builtin_amdgcn_raw_buffer_load_b16(v_rs, off, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kDaTile / RPI; i++) {
+      const int r = i * RPI + lane / CPR, c = (lane % CPR) ^ (r % CPR);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rs, (__attribute__((address_space(3))) void*)&sh.loop.ks[wave][i * 64],
+                                               16, ((t0 + r) * D + 8 * c) * 2, 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): V in registers, K in LDS
+    __builtin_amdgcn_wave_barrier();
+    u32x4 kv[CPR];
+#pragma unroll
+    for (int c = 0; c < CPR; c++) kv[c] = sh.loop.ks[wave][lane * CPR + (c ^ (lane % CPR))];
 
+    // logits: fp16 q . fp16 k with exact products and fp32 sums (v_dot2_f32_f16), then the
+    // log2(e) / sqrt(D) scale once per logit (the reference's log2-domain softmax, kernels.cuh:1522)
     float s[G];
 #pragma unroll
     for (int g = 0; g < G; g++) s[g] = 0.f;
 #pragma unroll
-    for (int c = 0; c < KC; c++) {
+    for (int c = 0; c < CPR; c++) {
 #pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const f16x2 kh = as_h2(kv[c][p]);
-        const float k0 = (float)kh.x, k1 = (float)kh.y;
+      for (int g = 0; g < G; g++) {
+        const u32x4 qv = qs[g][c];
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-          s[g] = __builtin_fmaf(qs[g][8 * c + 2 * p], k0, s[g]);
-          s[g] = __builtin_fmaf(qs[g][8 * c + 2 * p + 1], k1, s[g]);
-        }
+        for (int p = 0; p < 4; p++) s[g] = dot2(as_h2(qv[p]), as_h2(kv[c][p]), s[g]);
       }
     }
+#pragma unroll
+    for (int g = 0; g < G; g++) s[g] *= scale_log2;
     float p_[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -119,28 +161,52 @@ __global__ void __launch_bounds__(kDaWaves * 64) decode_attn_kernel(const f16* _
 #pragma unroll
       for (int d = 0; d < DPL; d++) o[g][d] *= a;
     }
+    // P.V: lane l owns dims l*DPL..; the weights go through LDS as fp16 pairs of consecutive keys
+    // (the precision of the reference's tensor-core path, which packs P to half for its MMA,
+    // kernels.cuh:1455-1460), and each pair of keys meets its two V values per dim in one
+    // v_dot2_f32_f16. A wave's LDS accesses complete in order, so its writes are visible to its
+    // later reads.
 #pragma unroll
-    for (int jj = 0; jj < kDaTile; jj++) {
-      if (jj < n) {  // uniform over the wave
-        float vf[DPL];
-        if constexpr (DPL == 2) {
-          const f16x2 vh = as_h2(vv[jj]);
-          vf[0] = (float)vh.x;
-          vf[1] = (float)vh.y;
-        } else {
-          vf[0] = (float)__builtin_bit_cast(f16, (uint16_t)vv[jj]);
-        }
+    for (int g = 0; g < G; g++) {
+      const float hi = __shfl_xor(p_[g], 1, 64);  // the neighbouring key's weight
+      if ((lane & 1) == 0) sh.loop.ps[wave][g][lane >> 1] = as_u32(f16x2{(f16)p_[g], (f16)hi});
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-          const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p_[g]), jj));
+    for (int j8 = 0; j8 < kDaTile; j8 += 8) {
+      if (j8 < n) {  // uniform over the wave; keys past n have p = 0 and V = 0
+        u32x4 pw[G];
 #pragma unroll
-          for (int d = 0; d < DPL; d++) o[g][d] = __builtin_fmaf(pj, vf[d], o[g][d]);
+        for (int g = 0; g < G; g++) pw[g] = *reinterpret_cast<const u32x4*>(&sh.loop.ps[wave][g][j8 / 2]);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int j = j8 + 2 * k;
+          if constexpr (DPL == 2) {
+            // (v_j[d0], v_j[d1]), (v_j+1[d0], v_j+1[d1]) -> (v_j[d0], v_j+1[d0]), (v_j[d1], v_j+1[d1])
+            const uint32_t a0 = vv[j], a1 = vv[j + 1];
+            const f16x2 v0 = as_h2(__builtin_amdgcn_perm(a1, a0, 0x05040100u));
+            const f16x2 v1 = as_h2(__builtin_amdgcn_perm(a1, a0, 0x07060302u));
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+              o[g][0] = dot2(as_h2(pw[g][k]), v0, o[g][0]);
+              o[g][1] = dot2(as_h2(pw[g][k]), v1, o[g][1]);
+            }
+          } else {
+            const f16x2 v0 = as_h2((uint32_t)vv[j] | ((uint32_t)vv[j + 1] << 16));
+#pragma unroll
+            for (int g = 0; g < G; g++) o[g][0] = dot2(as_h2(pw[g][k]), v0, o[g][0]);
+          }
         }
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   }
 
   // ---- merge the block's waves (a wave without keys has m = -inf and weight 0)
+  __syncthreads();  // every wave is done with the loop's LDS before it is reused
 #pragma unroll
   for (int g = 0; g < G; g++) {
     if (lane == 0) {
@@ -148,22 +214,22 @@ __global__ void __launch_bounds__(kDaWaves * 64) decode_attn_kernel(const f16* _
       wl[wave][g] = l[g];
     }
 #pragma unroll
-    for (int d = 0; d < DPL; d++) wo[wave][g][lane * DPL + d] = o[g][d];
+    for (int d = 0; d < DPL; d++) sh.merge.wo[wave][g][lane * DPL + d] = o[g][d];
   }
   __syncthreads();
   const bool single = S_eff == 1;
   float* po = part + (int64_t)kDecodeCounters;  // partials follow the counters (floats)
-  for (int i = tid; i < G * D; i += kDaWaves * 64) {
+  for (int i = tid; i < G * D; i += NT) {
     const int g = i / D, d = i % D;
     float M = -__builtin_huge_valf();
 #pragma unroll
-    for (int w = 0; w < kDaWaves; w++) M = fmaxf(M, wm[w][g]);
+    for (int w = 0; w < NWV; w++) M = fmaxf(M, wm[w][g]);
     float L = 0.f, O = 0.f;
 #pragma unroll
-    for (int w = 0; w < kDaWaves; w++) {
+    for (int w = 0; w < NWV; w++) {
       const float f = wm[w][g] == -__builtin_huge_valf() ? 0.f : exp2f(wm[w][g] - M);
       L = __builtin_fmaf(wl[w][g], f, L);
-      O = __builtin_fmaf(wo[w][g][d], f, O);
+      O = __builtin_fmaf(sh.merge.wo[w][g][d], f, O);
     }
     if (single) {
       out[(int64_t)b * ldo + (hk * G + g) * D + d] = (f16)(O / L);
@@ -187,19 +253,55 @@ __global__ void __launch_bounds__(kDaWaves * 64) decode_attn_kernel(const f16* _
   }
   __syncthreads();
   if (!is_last) return;
-  // ---- the last block merges the S_eff splits of every head of its group, in split order
-  for (int i = tid; i < G * D; i += kDaWaves * 64) {
-    const int g = i / D, d = i % D;
-    const float* pp = po + ((int64_t)b * Hq + hk * G + g) * kDecodeMaxSplits * (D + 2);
+  // ---- the last block merges the S_eff splits of every head of its group, in split order. The
+  //      (m, l) pairs and the first 16 splits' partial outputs are requested in one round; the
+  //      split weights exp2(m_s - M) / L are formed once per head while those loads are in flight.
+  constexpr int EPT = (G * D + NT - 1) / NT;  // output elements per thread
+  float v0[EPT][16];
+#pragma unroll
+  for (int e = 0; e < EPT; e++) {
+    const int i = tid + e * NT;
+    const int g = min(i / D, G - 1), d = i % D;
+    const float* pp = po + ((int64_t)b * Hq + hk * G + g) * kDecodeMaxSplits * (D + 2) + d;
+#pragma unroll
+    for (int k = 0; k < 16; k++) v0[e][k] = ld_coherent(pp + (int64_t)min(k, S_eff - 1) * (D + 2));
+  }
+  for (int i = tid; i < G * S_eff; i += NT) {
+    const int g = i / S_eff, s2 = i - g * S_eff;
+    const float* pp = po + (((int64_t)b * Hq + hk * G + g) * kDecodeMaxSplits + s2) * (D + 2);
+    sh.merge.sm[g][s2] = ld_coherent(pp + D);
+    sh.merge.sw[g][s2] = ld_coherent(pp + D + 1);
+  }
+  __syncthreads();
+  for (int g = wave; g < G; g += NWV) {
     float M = -__builtin_huge_valf();
-    for (int s2 = 0; s2 < S_eff; s2++) M = fmaxf(M, ld_coherent(pp + s2 * (D + 2) + D));
-    float L = 0.f, O = 0.f;
-    for (int s2 = 0; s2 < S_eff; s2++) {
-      const float f = exp2f(ld_coherent(pp + s2 * (D + 2) + D) - M);
-      L = __builtin_fmaf(ld_coherent(pp + s2 * (D + 2) + D + 1), f, L);
-      O = __builtin_fmaf(ld_coherent(pp + s2 * (D + 2) + d), f, O);
+    for (int s2 = lane; s2 < S_eff; s2 += 64) M = fmaxf(M, sh.merge.sm[g][s2]);
+    M = wave_max(M);
+    float Lp = 0.f;
+    for (int s2 = lane; s2 < S_eff; s2 += 64)
+      Lp = __builtin_fmaf(sh.merge.sw[g][s2], exp2f(sh.merge.sm[g][s2] - M), Lp);
+    const float Lt = wave_sum(Lp);
+    for (int s2 = lane; s2 < S_eff; s2 += 64) sh.merge.sw[g][s2] = exp2f(sh.merge.sm[g][s2] - M) / Lt;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < EPT; e++) {
+    const int i = tid + e * NT;
+    if (i < G * D) {
+      const int g = i / D, d = i % D;
+      const float* pp = po + ((int64_t)b * Hq + hk * G + g) * kDecodeMaxSplits * (D + 2) + d;
+      float O = 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; k++) O = __builtin_fmaf(v0[e][k], k < S_eff ? sh.merge.sw[g][k] : 0.f, O);
+      for (int s0 = 16; s0 < S_eff; s0 += 16) {
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) v[k] = ld_coherent(pp + (int64_t)min(s0 + k, S_eff - 1) * (D + 2));
+#pragma unroll
+        for (int k = 0; k < 16; k++) O = __builtin_fmaf(v[k], s0 + k < S_eff ? sh.merge.sw[g][s0 + k] : 0.f, O);
+      }
+      out[(int64_t)b * ldo + (hk * G + g) * D + d] = (f16)O;
     }
-    out[(int64_t)b * ldo + (hk * G + g) * D + d] = (f16)(O / L);
   }
 }
 
@@ -215,8 +317,8 @@ int decode_attn_d(int G, dim3 grid, hipStream_t s, const f16* q, int ldq, const 
                   int Hkv, const int* pos, float* part, int* counters, int S, f16* out, int ldo, float sl2) {
 #define HI_DA(g)                                                                                                      \
   case g:                                                                                                             \
-    hipLaunchKernelGGL((decode_attn_kernel<g, D>), grid, dim3(kDaWaves * 64), 0, s, q, ldq, kc, vc, max_seq, Hkv, pos, \
-                       part, counters, S, out, ldo, sl2, -1);                                                         \
+    hipLaunchKernelGGL((decode_attn_kernel<g, D, kDaWaves>), grid, dim3(kDaWaves * 64), 0, s, q, ldq, kc, vc, max_seq, \
+                       Hkv, pos, part, counters, S, out, ldo, sl2, -1);                                               \
     break;
   switch (G) {
     HI_DA(1) HI_DA(2) HI_DA(3) HI_DA(4) HI_DA(5) HI_DA(6) HI_DA(7) HI_DA(8)
@@ -311,8 +413,9 @@ HI_EXPORT int hi_decode_attn(const void* q, int ldq, const void* kc, const void*
   if (B == 0) return 0;
   if (B * Hkv > kDecodeCounters) HI_FAIL("hi_decode_attn: B*Hkv %d > %d", B * Hkv, kDecodeCounters);
   if (!q || !kc || !vc || !pos || !out || !work) HI_FAIL("hi_decode_attn: null pointer");
-  if (((uintptr_t)q & 1) || ((uintptr_t)kc & 15) || ((uintptr_t)vc & 15) || ((uintptr_t)work & 3) || (((uintptr_t)out) & 1))
-    HI_FAIL("hi_decode_attn: kc and vc must be 16-byte aligned");
+  if (((uintptr_t)q & 15) || ldq % 8 || ((uintptr_t)kc & 15) || ((uintptr_t)vc & 15) || ((uintptr_t)work & 3) ||
+      (((uintptr_t)out) & 1))
+    HI_FAIL("hi_decode_attn: q, kc and vc must be 16-byte aligned and ldq a multiple of 8");
   if (ldq < Hq * D || ldo < Hq * D) HI_FAIL("hi_decode_attn: ldq %d / ldo %d < Hq * D = %d", ldq, ldo, Hq * D);
   const int S = decode_splits(B, Hkv, d->cus);
   const float sl2 = 1.4426950408889634f / sqrtf((float)D);
