@@ -1,7 +1,7 @@
 """ctypes host for libhipinfer.so: the matmul hot path of hipinfer on torch tensors.
 
 Mirrors the kernel-level functions of the reference's scripts/hipinfer.py (gemv, gemv_qkv_rope,
-gemm, moe_router, moe_experts, rmsnorm; hipinfer.py:101-161, 288-306) with the same names,
+gemm, moe_router, moe_experts, rmsnorm, decode_attn; hipinfer.py:101-190, 288-306) with the same names,
 arguments and defaults, over the same hi_* C symbols, plus the int8 quantiser of
 scripts/export.py:54-101 (quantize_rows, dequantize_rows, interleave_gate_up) running on the GPU.
 torch is only the container for device memory and the current stream.
