@@ -101,10 +101,19 @@ __device__ __forceinline__ void store4(f16* p, f16x4 v, bool vec) {
   }
 }
 
-// Half offset of logical 16-byte chunk `c` of row `r` in an LDS tile of 64-half (128-byte) rows.
-__device__ __forceinline__ int lds_off(int r, int c) { return r * kGemmBK + ((c ^ ((r >> 1) & 7)) << 3); }
-// Byte offset of logical 16-byte chunk `c` of row `r` in an LDS tile of 64-byte int8 rows.
-__device__ __forceinline__ int lds_off8(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+// Half offset of logical 16-byte chunk `c` of row `r` in an LDS tile of BK-half rows (128 or 64
+// bytes): the XOR term spreads the 16 rows one 128-bit read serves per cycle over all 64 banks.
+template <int BK>
+__device__ __forceinline__ int lds_off(int r, int c) {
+  if constexpr (BK == 64) return r * 64 + ((c ^ ((r >> 1) & 7)) << 3);
+  else return r * 32 + ((c ^ ((r >> 2) & 3)) << 3);
+}
+// Byte offset of logical 16-byte chunk `c` of row `r` in an LDS tile of BK-byte int8 rows.
+template <int BK>
+__device__ __forceinline__ int lds_off8(int r, int c) {
+  if constexpr (BK == 64) return r * 64 + ((c ^ ((r >> 2) & 3)) << 4);
+  else return r * 32 + ((c ^ ((r >> 3) & 1)) << 4);
+}
 
 // Scheduling pattern of one step: the step's NM MFMAs alternate with the ND LDS reads of the next
 // step's fragments (then whichever is left over), so the reads are issued early and their latency
@@ -121,20 +130,25 @@ __device__ __forceinline__ void sched_step() {
   if constexpr (ND > P) __builtin_amdgcn_sched_group_barrier(0x100, ND - P, 0);
 }
 
-template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, bool GRP = false>
+template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, bool GRP = false, int BK = 64>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   constexpr int TM = BM / WM, TN = BN / WN;          // wave tile
   constexpr int FM = TM / 32, FN = TN / 32;          // MFMA tiles per wave
-  constexpr int A_ST = BM * kGemmBK;                 // halves per stage
-  constexpr int B_ROWB = Q8 ? 64 : 128;              // bytes of one W row per K tile
+  constexpr int A_ST = BM * BK;                      // halves per stage
+  constexpr int B_ROWB = Q8 ? BK : 2 * BK;           // bytes of one W row per K tile
+  constexpr int RPI = 512 / BK;                      // fp16 rows per 1 KB DMA instruction
+  constexpr int RPI8 = 1024 / BK;                    // int8 rows per 1 KB DMA instruction
   constexpr int B_ST = BN * B_ROWB / 2;              // halves per stage
   constexpr int NW = WM * WN;                        // waves per block (4 or 8)
-  constexpr int A_LD = BM * 128 / 1024 / NW;         // 1 KB DMA instructions per wave per K tile (A)
+  constexpr int A_LD = BM * 2 * BK / 1024 / NW;      // 1 KB DMA instructions per wave per K tile (A)
   constexpr int B_LD = BN * B_ROWB / 1024 / NW;      // ... (W)
   constexpr int L = A_LD + B_LD;                     // vector-memory ops per lane per K tile
   static_assert((NW == 4 || NW == 8) && FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tiling");
-  static_assert(A_LD >= 1 && B_LD >= 1 && S >= 2 && S <= 4 && 3 * L < 64, "pipeline shape");
+  static_assert(A_LD >= 1 && B_LD >= 1 && A_LD * 1024 * NW == BM * 2 * BK && B_LD * 1024 * NW == BN * B_ROWB &&
+                    S >= 2 && S <= 8 && (S - 1) * L < 64 && 3 * L < 64,
+                "pipeline shape: every wave issues the same whole number of 1 KB DMA instructions");
   static_assert(!(GRP && Q8), "grouped (expert) GEMMs take fp16 weights");
+  static_assert(BK == 64 || BK == 32, "K tile depth");
   // The dynamic LDS follows the static (the split-K flag below); a 16-byte element type makes the
   // compiler start it on a 16-byte boundary, which every 128-bit LDS access and DMA here needs.
   extern __shared__ u32x4 smem_raw[];
@@ -186,10 +200,11 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   }
   const int bm = tm * BM, bn = tn * BN;
 
-  const int nkt = (K + kGemmBK - 1) / kGemmBK;
+  const int nkt = (K + BK - 1) / BK;
   const int kt0 = blockIdx.y * g.kt_per_split;
   const int nloc = min(nkt, kt0 + g.kt_per_split) - kt0;  // K tiles of this split (>= 1)
-  const bool half_tail = (K & 63) != 0 && kt0 + nloc == nkt;  // the last tile holds only 32 k
+  // the last tile holds only 32 k (K % 64 == 32 with 64-deep tiles; K % 32 == 0 always)
+  const bool half_tail = BK == 64 && (K & 63) != 0 && kt0 + nloc == nkt;
 
   // ---- DMA of one K tile into stage st, through buffer resources based at the block's first A
   //      and W rows. Lane l of an instruction covering 8 (A, W fp16) or 16 (W int8) rows fills LDS
@@ -205,34 +220,40 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
       0x00020000);
   // this lane's byte offset within an instruction's rows; the swizzle term of a 128-byte row r is
   // ((r >> 1) & 7), which over an instruction's 8 rows depends on the instruction's parity and
-  // lane / 16; for 64-byte int8 rows, ((r >> 2) & 3) depends on lane / 16 only
-  const int a_r = lane >> 3, a_p = lane & 7;
+  // lane / 16; of a 64-byte row ((r >> 2) & 3) and of a 32-byte int8 row ((r >> 3) & 1), which
+  // depend on the lane only
+  const int a_r = lane / (BK / 8), a_p = lane % (BK / 8);
   int a_lo[2], b_lo[2];
 #pragma unroll
   for (int par = 0; par < 2; par++) {
-    const int sw = (par * 4 + (a_r >> 1)) & 7;
+    const int sw = BK == 64 ? (par * 4 + (a_r >> 1)) & 7 : (a_r >> 2) & 3;
     a_lo[par] = (int)((int64_t)a_r * g.lda * 2) + ((a_p ^ sw) << 4);
-    b_lo[par] = Q8 ? (lane >> 2) * K + (((lane & 3) ^ ((lane >> 4) & 3)) << 4) : a_r * K * 2 + ((a_p ^ sw) << 4);
+    if constexpr (Q8) {
+      b_lo[par] = BK == 64 ? (lane >> 2) * K + (((lane & 3) ^ ((lane >> 4) & 3)) << 4)
+                           : (lane >> 1) * K + (((lane & 1) ^ ((lane >> 4) & 1)) << 4);
+    } else {
+      b_lo[par] = a_r * K * 2 + ((a_p ^ sw) << 4);
+    }
   }
   auto issue = [&](int kt, int st) {
-    const int k0 = kt * kGemmBK;
+    const int k0 = kt * BK;
     f16* as = As + st * A_ST;
 #pragma unroll
     for (int i = 0; i < A_LD; i++) {
-      const int ri = (wave * A_LD + i) * 8;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_void_t*)(as + ri * kGemmBK), 16,
-                                               a_lo[ri >> 3 & 1] + (int)((int64_t)ri * g.lda * 2) + k0 * 2, 0, 0, 0);
+      const int ri = (wave * A_LD + i) * RPI;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_void_t*)(as + ri * BK), 16,
+                                               a_lo[(ri / RPI) & 1] + (int)((int64_t)ri * g.lda * 2) + k0 * 2, 0, 0, 0);
     }
     char* bs = reinterpret_cast<char*>(Bs + st * B_ST);
 #pragma unroll
     for (int i = 0; i < B_LD; i++) {
       if constexpr (Q8) {
-        const int ri = (wave * B_LD + i) * 16;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rs, (lds_void_t*)(bs + ri * 64), 16, b_lo[0] + ri * K + k0, 0, 0, 0);
+        const int ri = (wave * B_LD + i) * RPI8;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rs, (lds_void_t*)(bs + ri * BK), 16, b_lo[0] + ri * K + k0, 0, 0, 0);
       } else {
-        const int ri = (wave * B_LD + i) * 8;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rs, (lds_void_t*)(bs + ri * 128), 16,
-                                                 b_lo[ri >> 3 & 1] + ri * K * 2 + k0 * 2, 0, 0, 0);
+        const int ri = (wave * B_LD + i) * RPI;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rs, (lds_void_t*)(bs + ri * 2 * BK), 16,
+                                                 b_lo[(ri / RPI) & 1] + ri * K * 2 + k0 * 2, 0, 0, 0);
       }
     }
   };
@@ -260,21 +281,21 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
     const int c = 4 * (s >> 1) + 2 * fk + (s & 1);
     const f16* as = As + st * A_ST;
 #pragma unroll
-    for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const f16x8*>(as + lds_off(a_row[i], c));
+    for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const f16x8*>(as + lds_off<BK>(a_row[i], c));
   };
   // fp16 W: one fragment per step
   auto load_b = [&](int st, int s, f16x8 (&bf)[FN]) {
     const int c = 4 * (s >> 1) + 2 * fk + (s & 1);
     const f16* bs = Bs + st * B_ST;
 #pragma unroll
-    for (int j = 0; j < FN; j++) bf[j] = *reinterpret_cast<const f16x8*>(bs + lds_off(b_row[j], c));
+    for (int j = 0; j < FN; j++) bf[j] = *reinterpret_cast<const f16x8*>(bs + lds_off<BK>(b_row[j], c));
   };
   // int8 W: both steps of half jh as one raw 16-byte chunk
   auto load_q = [&](int st, int jh, u32x4 (&bq)[FN]) {
     const char* bs = reinterpret_cast<const char*>(Bs + st * B_ST);
     const int c = 2 * jh + fk;
 #pragma unroll
-    for (int j = 0; j < FN; j++) bq[j] = *reinterpret_cast<const u32x4*>(bs + lds_off8(b_row[j], c));
+    for (int j = 0; j < FN; j++) bq[j] = *reinterpret_cast<const u32x4*>(bs + lds_off8<BK>(b_row[j], c));
   };
 
   f32x16 acc[FM][FN];
@@ -325,53 +346,86 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
 
   constexpr int NM = FM * FN;               // MFMAs per step
   constexpr int ND = FM + (Q8 ? 0 : FN);    // LDS reads per step (int8 W: + FN every other step)
-  // ---- main loop over all tiles but the last: 4 steps each, fragments one step ahead
-  for (int t = 0; t < nloc - 1; t++) {
-    const int st = t % S;
-    load_a(st, 1, af1);
-    if constexpr (!Q8) load_b(st, 1, bf1);
-    mfmas(0, af0, bf0, bq0);
-    sched_step<NM, ND>();
-    load_a(st, 2, af0);
-    if constexpr (Q8) load_q(st, 1, bq1);
-    else load_b(st, 2, bf0);
-    mfmas(1, af1, bf1, bq0);
-    sched_step<NM, ND + (Q8 ? FN : 0)>();
-    load_a(st, 3, af1);
-    if constexpr (!Q8) load_b(st, 3, bf1);
-    mfmas(0, af0, bf0, bq1);
-    sched_step<NM, ND>();
-    // the tile's last fragments are in registers: free its stage, refill it, start the next tile
-    wait_lgkm0();
-    wait_vmcnt<(S - 2) * L>();
-    barrier_no_fence();
-    issue(tile_or_first(kt0 + t + S), st);
-    const int sn = (t + 1) % S;
-    load_a(sn, 0, af0);
-    if constexpr (Q8) load_q(sn, 0, bq0);
-    else load_b(sn, 0, bf0);
-    mfmas(1, af1, bf1, bq1);
-    sched_step<NM, ND + (Q8 ? FN : 0)>();
-  }
-  // ---- the last tile (its first half only when K % 64 == 32)
-  {
+  if constexpr (BK == 64) {
+    // ---- main loop over all tiles but the last: 4 steps each, fragments one step ahead
+    for (int t = 0; t < nloc - 1; t++) {
+      const int st = t % S;
+      load_a(st, 1, af1);
+      if constexpr (!Q8) load_b(st, 1, bf1);
+      mfmas(0, af0, bf0, bq0);
+      sched_step<NM, ND>();
+      load_a(st, 2, af0);
+      if constexpr (Q8) load_q(st, 1, bq1);
+      else load_b(st, 2, bf0);
+      mfmas(1, af1, bf1, bq0);
+      sched_step<NM, ND + (Q8 ? FN : 0)>();
+      load_a(st, 3, af1);
+      if constexpr (!Q8) load_b(st, 3, bf1);
+      mfmas(0, af0, bf0, bq1);
+      sched_step<NM, ND>();
+      // the tile's last fragments are in registers: free its stage, refill it, start the next tile
+      wait_lgkm0();
+      wait_vmcnt<(S - 2) * L>();
+      barrier_no_fence();
+      issue(tile_or_first(kt0 + t + S), st);
+      const int sn = (t + 1) % S;
+      load_a(sn, 0, af0);
+      if constexpr (Q8) load_q(sn, 0, bq0);
+      else load_b(sn, 0, bf0);
+      mfmas(1, af1, bf1, bq1);
+      sched_step<NM, ND + (Q8 ? FN : 0)>();
+    }
+    // ---- the last tile (its first half only when K % 64 == 32)
+    {
+      const int st = (nloc - 1) % S;
+      load_a(st, 1, af1);
+      if constexpr (!Q8) load_b(st, 1, bf1);
+      mfmas(0, af0, bf0, bq0);
+      mfmas(1, af1, bf1, bq0);
+      if (!half_tail) {
+        load_a(st, 2, af0);
+        load_a(st, 3, af1);
+        if constexpr (Q8) {
+          load_q(st, 1, bq1);
+        } else {
+          load_b(st, 2, bf0);
+          load_b(st, 3, bf1);
+        }
+        mfmas(0, af0, bf0, bq1);
+        mfmas(1, af1, bf1, bq1);
+      }
+    }
+  } else {
+    // ---- 32-deep tiles: 2 steps each, fragments one step ahead; int8 W holds both steps of a
+    //      tile in one raw 16-byte chunk per fragment (bq0), the next tile's read into bqn first
+    for (int t = 0; t < nloc - 1; t++) {
+      const int st = t % S;
+      load_a(st, 1, af1);
+      if constexpr (!Q8) load_b(st, 1, bf1);
+      mfmas(0, af0, bf0, bq0);
+      sched_step<NM, ND>();
+      // the tile's last fragments are in registers: free its stage, refill it, start the next tile
+      wait_lgkm0();
+      wait_vmcnt<(S - 2) * L>();
+      barrier_no_fence();
+      issue(tile_or_first(kt0 + t + S), st);
+      const int sn = (t + 1) % S;
+      load_a(sn, 0, af0);
+      [[maybe_unused]] u32x4 bqn[FN];
+      if constexpr (Q8) load_q(sn, 0, bqn);
+      else load_b(sn, 0, bf0);
+      mfmas(1, af1, bf1, bq0);
+      sched_step<NM, ND + (Q8 ? FN : 0)>();
+      if constexpr (Q8) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) bq0[j] = bqn[j];
+      }
+    }
     const int st = (nloc - 1) % S;
     load_a(st, 1, af1);
     if constexpr (!Q8) load_b(st, 1, bf1);
     mfmas(0, af0, bf0, bq0);
     mfmas(1, af1, bf1, bq0);
-    if (!half_tail) {
-      load_a(st, 2, af0);
-      load_a(st, 3, af1);
-      if constexpr (Q8) {
-        load_q(st, 1, bq1);
-      } else {
-        load_b(st, 2, bf0);
-        load_b(st, 3, bf1);
-      }
-      mfmas(0, af0, bf0, bq1);
-      mfmas(1, af1, bf1, bq1);
-    }
   }
   wait_vmcnt<0>();  // the refills issued past the last tile have landed before the block ends
 
@@ -477,29 +531,43 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(const float* __restric
   store4(dst, o, vec_c);
 }
 
-// Tile configurations (BK = 64): {BM, BN, WM, WN, stages}; WM x WN waves per block.
+// Tile configurations: {BM, BN, WM, WN, stages, BK}; WM x WN waves per block, BK-deep K tiles. The
+// 32-deep ones give the big 8-wave tiles four (or six) stages in the same LDS as two 64-deep
+// ones: more K tiles in flight to cover the global->LDS latency. 128 x 160 and 128 x 96 (four
+// waves stacked along M, each 32 rows by the whole width) cut N = 5120 and N = 3072 at M = 1024
+// into exactly 256 tiles, one per CU, with no split-K.
 struct GemmCfg {
-  int bm, bn, wm, wn, st;
+  int bm, bn, wm, wn, st, bk;
 };
-constexpr GemmCfg kGemmCfgs[] = {{256, 256, 2, 2, 2}, {256, 128, 2, 2, 3}, {128, 256, 2, 2, 3}, {64, 128, 2, 2, 4},
-                                 {128, 128, 2, 2, 2}, {64, 64, 2, 2, 4},   {32, 128, 1, 4, 4}, {128, 64, 2, 2, 4},
-                                 {256, 256, 2, 4, 2}, {256, 128, 2, 4, 3}};
+constexpr GemmCfg kGemmCfgs[] = {{256, 256, 2, 2, 2, 64}, {256, 128, 2, 2, 3, 64}, {128, 256, 2, 2, 3, 64},
+                                 {64, 128, 2, 2, 4, 64},  {128, 128, 2, 2, 2, 64}, {64, 64, 2, 2, 4, 64},
+                                 {32, 128, 1, 4, 4, 64},  {128, 64, 2, 2, 4, 64},  {256, 256, 2, 4, 2, 64},
+                                 {256, 128, 2, 4, 3, 64}, {256, 256, 2, 4, 4, 32}, {256, 128, 2, 2, 6, 32},
+                                 {128, 256, 2, 4, 6, 32}, {128, 160, 4, 1, 4, 64}, {128, 96, 4, 1, 4, 64}};
 constexpr int kGemmNumCfgs = sizeof(kGemmCfgs) / sizeof(kGemmCfgs[0]);
+// A config exists for a weight format when its A and W tiles split into whole 1 KB DMA
+// instructions per wave (int8 W rows are half as wide: 128 x 160 and 128 x 96 are fp16 only).
+constexpr bool gemm_cfg_ok(int c, bool q8) {
+  const int nw = kGemmCfgs[c].wm * kGemmCfgs[c].wn, bk = kGemmCfgs[c].bk;
+  const int a = kGemmCfgs[c].bm * 2 * bk, b = kGemmCfgs[c].bn * (q8 ? bk : 2 * bk);
+  return a % (1024 * nw) == 0 && b % (1024 * nw) == 0 && a >= 1024 * nw && b >= 1024 * nw;
+}
 constexpr int kGemmGrpCfg = 3;  // the grouped (MoE expert) GEMM's tile: 64 x 128
 inline size_t gemm_lds_bytes(int cfg, bool q8) {
   const GemmCfg& c = kGemmCfgs[cfg];
-  return (size_t)c.st * (c.bm * kGemmBK * 2 + c.bn * (q8 ? 64 : 128));
+  return (size_t)c.st * (c.bm * c.bk * 2 + c.bn * (q8 ? c.bk : 2 * c.bk));
 }
 
-template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8>
+template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, int BK>
 int gemm_launch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
   const size_t lds = gemm_lds_bytes(cfg, Q8);
-  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WM, WN, S, EPI, Q8>);
+  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WM, WN, S, EPI, Q8, false, BK>);
   const int bpc = hi_blocks_per_cu(fn, 64 * WM * WN, lds);  // also lifts the dynamic-LDS limit
   if (bpc < 0) return -2;
   if (bpc == 0) HI_FAIL("gemm: tile %dx%d does not fit on a CU", BM, BN);
   const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, EPI, Q8>), dim3(tiles, splits), dim3(64 * WM * WN), lds, s, g);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, EPI, Q8, false, BK>), dim3(tiles, splits), dim3(64 * WM * WN), lds,
+                     s, g);
   HI_TRY(hipGetLastError());
   if (splits > 1) {
     const int64_t quads = (int64_t)g.M * (EPI == 2 ? g.N / 2 : g.N) / 4;
@@ -517,32 +585,43 @@ int gemm_run(const GemmArgs& g, int cfg, int splits, bool q8, hipStream_t s);
 template <int EPI>
 int gemm_blocks_per_cu(int cfg, bool q8);
 
-#define HI_GEMM_K(i, q) gemm_kernel<kGemmCfgs[i].bm, kGemmCfgs[i].bn, kGemmCfgs[i].wm, kGemmCfgs[i].wn, kGemmCfgs[i].st, EPI, q>
+#define HI_GEMM_K(i, q)                                                                                        \
+  gemm_kernel<kGemmCfgs[i].bm, kGemmCfgs[i].bn, kGemmCfgs[i].wm, kGemmCfgs[i].wn, kGemmCfgs[i].st, EPI, q, false, \
+              kGemmCfgs[i].bk>
 #define HI_GEMM_CFG(i, q)                                                                                      \
-  if (cfg == i && q8 == q)                                                                                     \
-    return gemm_launch<kGemmCfgs[i].bm, kGemmCfgs[i].bn, kGemmCfgs[i].wm, kGemmCfgs[i].wn, kGemmCfgs[i].st, EPI, q>( \
-        g, cfg, splits, s);
+  if constexpr (gemm_cfg_ok(i, q)) {                                                                           \
+    if (cfg == i && q8 == q)                                                                                   \
+      return gemm_launch<kGemmCfgs[i].bm, kGemmCfgs[i].bn, kGemmCfgs[i].wm, kGemmCfgs[i].wn, kGemmCfgs[i].st, EPI, \
+                         q, kGemmCfgs[i].bk>(g, cfg, splits, s);                                               \
+  }
 #define HI_GEMM_OCC(i)                                                                                         \
-  if (cfg == i)                                                                                                \
-    return hi_blocks_per_cu(q8 ? reinterpret_cast<const void*>(&HI_GEMM_K(i, true))                            \
-                               : reinterpret_cast<const void*>(&HI_GEMM_K(i, false)),                          \
-                            64 * kGemmCfgs[i].wm * kGemmCfgs[i].wn, gemm_lds_bytes(i, q8));
+  if constexpr (gemm_cfg_ok(i, true))                                                                          \
+    if (cfg == i && q8)                                                                                        \
+      return hi_blocks_per_cu(reinterpret_cast<const void*>(&HI_GEMM_K(i, true)),                              \
+                              64 * kGemmCfgs[i].wm * kGemmCfgs[i].wn, gemm_lds_bytes(i, true));                \
+  if constexpr (gemm_cfg_ok(i, false))                                                                         \
+    if (cfg == i && !q8)                                                                                       \
+      return hi_blocks_per_cu(reinterpret_cast<const void*>(&HI_GEMM_K(i, false)),                             \
+                              64 * kGemmCfgs[i].wm * kGemmCfgs[i].wn, gemm_lds_bytes(i, false));
 #define HI_GEMM_DEFINE_RUN(EPIV)                                                                               \
   template <>                                                                                                  \
   int gemm_run<EPIV>(const GemmArgs& g, int cfg, int splits, bool q8, hipStream_t s) {                        \
     constexpr int EPI = EPIV;                                                                                  \
     HI_GEMM_CFG(0, false) HI_GEMM_CFG(1, false) HI_GEMM_CFG(2, false) HI_GEMM_CFG(3, false)                    \
     HI_GEMM_CFG(4, false) HI_GEMM_CFG(5, false) HI_GEMM_CFG(6, false) HI_GEMM_CFG(7, false)                    \
-    HI_GEMM_CFG(8, false) HI_GEMM_CFG(9, false)                                                                \
+    HI_GEMM_CFG(8, false) HI_GEMM_CFG(9, false) HI_GEMM_CFG(10, false) HI_GEMM_CFG(11, false)                  \
+    HI_GEMM_CFG(12, false) HI_GEMM_CFG(13, false) HI_GEMM_CFG(14, false)                                       \
     HI_GEMM_CFG(0, true) HI_GEMM_CFG(1, true) HI_GEMM_CFG(2, true) HI_GEMM_CFG(3, true)                        \
     HI_GEMM_CFG(4, true) HI_GEMM_CFG(5, true) HI_GEMM_CFG(6, true) HI_GEMM_CFG(7, true)                        \
-    HI_GEMM_CFG(8, true) HI_GEMM_CFG(9, true)                                                                  \
+    HI_GEMM_CFG(8, true) HI_GEMM_CFG(9, true) HI_GEMM_CFG(10, true) HI_GEMM_CFG(11, true) HI_GEMM_CFG(12, true) \
+    HI_GEMM_CFG(13, true) HI_GEMM_CFG(14, true)                                                                \
     HI_FAIL("gemm: no kernel for config %d", cfg);                                                             \
   }                                                                                                            \
   template <>                                                                                                  \
   int gemm_blocks_per_cu<EPIV>(int cfg, bool q8) {                                                             \
     constexpr int EPI = EPIV;                                                                                  \
     HI_GEMM_OCC(0) HI_GEMM_OCC(1) HI_GEMM_OCC(2) HI_GEMM_OCC(3) HI_GEMM_OCC(4) HI_GEMM_OCC(5) HI_GEMM_OCC(6)    \
-    HI_GEMM_OCC(7) HI_GEMM_OCC(8) HI_GEMM_OCC(9)                                                               \
+    HI_GEMM_OCC(7) HI_GEMM_OCC(8) HI_GEMM_OCC(9) HI_GEMM_OCC(10) HI_GEMM_OCC(11) HI_GEMM_OCC(12)              \
+    HI_GEMM_OCC(13) HI_GEMM_OCC(14)                                                                            \
     return -1;                                                                                                 \
   }

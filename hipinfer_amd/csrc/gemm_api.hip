@@ -49,7 +49,7 @@ int cfg_blocks_per_cu(int cfg, bool q8) {
 }
 
 // Relative MFMA efficiency of each tile shape (bigger tiles reuse more of what they stage).
-constexpr double kCfgEff[kGemmNumCfgs] = {0.9, 0.85, 0.85, 0.6, 0.8, 0.45, 0.4, 0.6, 1.0, 0.9};
+constexpr double kCfgEff[kGemmNumCfgs] = {0.9, 0.85, 0.85, 0.6, 0.8, 0.45, 0.4, 0.6, 1.0, 0.9, 1.05, 0.85, 0.95, 0.85, 0.8};
 
 struct Choice {
   int cfg, splits;
@@ -61,19 +61,20 @@ struct Choice {
 Choice gemm_pick(int M, int N, int K, bool q8, int cus) {
   Choice best{1, 1};
   double best_t = 1e300;
-  const int nkt = (K + kGemmBK - 1) / kGemmBK;
   const double mfma_per_cu = 4069.0 * 2.4e9;  // fp16 flop/s per CU at the datasheet peak
   const double l2_bw = 20e12;                 // aggregate L2/MALL bytes/s the staging can draw
   for (int c = 0; c < kGemmNumCfgs; c++) {
-    const int bm = kGemmCfgs[c].bm, bn = kGemmCfgs[c].bn;
+    if (!gemm_cfg_ok(c, q8)) continue;
+    const int bm = kGemmCfgs[c].bm, bn = kGemmCfgs[c].bn, bk = kGemmCfgs[c].bk;
+    const int nkt = (K + bk - 1) / bk;
     const double tiles = (double)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int slots = cus * cfg_blocks_per_cu(c, q8);
     for (int sp = 1; sp <= 8; sp *= 2) {
       if (sp > nkt || (sp > 1 && tiles * sp > 4.0 * cus) || tiles > kMaxTiles) continue;
       const int kps = (nkt + sp - 1) / sp;
       const double rounds = std::ceil(tiles * sp / slots);
-      const double t_mfma = rounds * 2.0 * bm * bn * kps * kGemmBK / (mfma_per_cu * kCfgEff[c]);
-      const double t_l2 = tiles * sp * kps * (double)(bm * 128 + bn * (q8 ? 64 : 128)) / l2_bw;
+      const double t_mfma = rounds * 2.0 * bm * bn * kps * bk / (mfma_per_cu * kCfgEff[c]);
+      const double t_l2 = tiles * sp * kps * (double)(bm * 2 * bk + bn * (q8 ? bk : 2 * bk)) / l2_bw;
       double t = std::max(t_mfma, t_l2) + 2e-6;
       if (sp > 1) t += (double)M * N * sp * 8.0 / 4e12 + 3e-6;  // partials out and back, second launch
       if (t < best_t) {
@@ -179,11 +180,12 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
     *us = ms * 1e3f / reps;
     return 0;
   };
-  const int nkt = (g.K + kGemmBK - 1) / kGemmBK;
   std::vector<std::pair<float, Choice>> timed;
   int rc = 0;
   for (int c = 0; c < kGemmNumCfgs && !rc; c++) {
+    if (!gemm_cfg_ok(c, q8)) continue;
     const int bm = kGemmCfgs[c].bm, bn = kGemmCfgs[c].bn;
+    const int nkt = (g.K + kGemmCfgs[c].bk - 1) / kGemmCfgs[c].bk;
     const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
     if (bm > 2 * mb && kGemmCfgs[c].bm != 32) continue;  // a tile far taller than M only stages padding
     for (int sp = 1; sp <= 8 && !rc; sp *= 2) {
@@ -228,7 +230,7 @@ int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s
   const HiDevice* d = hi_device();
   if (!d) return -2;
   GemmArgs g = g0;
-  const int nkt = (g.K + kGemmBK - 1) / kGemmBK;
+  const int nkt = (g.K + kGemmCfgs[ch.cfg].bk - 1) / kGemmCfgs[ch.cfg].bk;  // K tiles of the chosen depth
   if (ch.splits > nkt) ch.splits = nkt;
   int kps = (nkt + ch.splits - 1) / ch.splits;
   ch.splits = (nkt + kps - 1) / kps;  // no empty splits
@@ -287,7 +289,7 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
   g.K = K;
   g.vec_c = aligned(C, 8) && ldc % 4 == 0;
   Choice ch{1, 1};
-  if (g_force_cfg >= 0 && g_force_cfg < kGemmNumCfgs) {
+  if (g_force_cfg >= 0 && g_force_cfg < kGemmNumCfgs && gemm_cfg_ok(g_force_cfg, q8)) {  // else: automatic
     ch = gemm_pick(M, N, K, q8, d->cus);
     ch.cfg = g_force_cfg;
   } else if (int r = gemm_choose(g, epi, q8, s, &ch)) {
@@ -325,7 +327,7 @@ HI_EXPORT int hi_gemm_force_splits(int sp) {
 HI_EXPORT int hi_gemm_num_configs() { return kGemmNumCfgs; }
 HI_EXPORT int hi_gemm_config_desc(int c, char* out, int n) {
   if (c < 0 || c >= kGemmNumCfgs || !out || n < 1) return -1;
-  snprintf(out, n, "mfma 32x32x16 %dx%dx%d waves %dx%d stages %d", kGemmCfgs[c].bm, kGemmCfgs[c].bn, kGemmBK,
+  snprintf(out, n, "mfma 32x32x16 %dx%dx%d waves %dx%d stages %d", kGemmCfgs[c].bm, kGemmCfgs[c].bn, kGemmCfgs[c].bk,
            kGemmCfgs[c].wm, kGemmCfgs[c].wn, kGemmCfgs[c].st);
   return 0;
 }

@@ -319,7 +319,8 @@ template <int EPI>
 int grouped_gemm(const f16* A, int lda, const f16* W, int64_t wstride_bytes, f16* C, int ldc, int N, int K,
                  const int* off, const int* tiles, int E, int max_row_tiles, hipStream_t s) {
   constexpr int cfg = kGemmGrpCfg;
-  static_assert(kGemmCfgs[cfg].bm == kGrpBM && kGemmCfgs[cfg].bn == kGrpBN, "grouped tile");
+  static_assert(kGemmCfgs[cfg].bm == kGrpBM && kGemmCfgs[cfg].bn == kGrpBN && kGemmCfgs[cfg].bk == kGemmBK,
+                "grouped tile");
   GemmArgs g{};
   g.A = A;
   g.lda = lda;

@@ -55,12 +55,22 @@ def gemm_check(hi, O, name, A, W, r, epi=0, bias=None, scales=None, res=None, to
     torch.cuda.synchronize()
 
 
+# every tile configuration (the automatic choice is -1); configs past the library's count skip
+CFGS = [-1] + list(range(15))
+
+
+def need_cfg(hi, cfg):
+    if cfg >= hi.lib.hi_gemm_num_configs():
+        pytest.skip(f"the library has {hi.lib.hi_gemm_num_configs()} configs")
+
+
 SHAPES = [(128, 2560, 2048), (77, 2048, 5632), (512, 32000, 2048), (1000, 2048, 2048), (300, 1152, 896),
           (64, 6144, 4096), (257, 4096, 14336)]
 
 
-@pytest.mark.parametrize("cfg", [-1, 0, 1, 2, 3, 4, 5, 6])
+@pytest.mark.parametrize("cfg", CFGS)
 def test_gemm_configs(hi, O, cfg):
+    need_cfg(hi, cfg)
     r = rng(300 + cfg)
     hi.lib.hi_gemm_force_config(cfg)
     try:
@@ -128,7 +138,7 @@ def test_gemm_short_k(hi, O):
     tiles leaves no empty split."""
     r = rng(330)
     try:
-        for cfg in [-1, 0, 1, 5, 6]:
+        for cfg in [-1, 0, 1, 5, 6, 10, 12, 13, 14]:
             hi.lib.hi_gemm_force_config(cfg)
             for sp in [1, 2]:
                 hi.lib.hi_gemm_force_splits(sp)
@@ -141,8 +151,9 @@ def test_gemm_short_k(hi, O):
         hi.lib.hi_gemm_force_splits(-1)
 
 
-@pytest.mark.parametrize("cfg", [-1, 0, 1, 2, 3, 4, 5, 6])
+@pytest.mark.parametrize("cfg", CFGS)
 def test_gemm_int8(hi, O, cfg):
+    need_cfg(hi, cfg)
     r = rng(340 + cfg)
     H, I = 2048, 5632
     hi.lib.hi_gemm_force_config(cfg)
