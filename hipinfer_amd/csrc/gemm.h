@@ -474,6 +474,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           const int col = c0 + 8 * q + 4 * fk;
+          if (col >= N) continue;  // N % 16 == 0: the last 32-column tile can end 16 columns past N
           f16x4 o;
           if constexpr (EPI == 1) {
             const f16x4 r = load4(crow + col, g.vec_c);
@@ -535,7 +536,8 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(const float* __restric
 // 32-deep ones give the big 8-wave tiles four (or six) stages in the same LDS as two 64-deep
 // ones: more K tiles in flight to cover the global->LDS latency. 128 x 160 and 128 x 96 (four
 // waves stacked along M, each 32 rows by the whole width) cut N = 5120 and N = 3072 at M = 1024
-// into exactly 256 tiles, one per CU, with no split-K.
+// into exactly 256 tiles, one per CU, with no split-K. 32 x 256 (four waves side by side, 32 x 64
+// each) serves batched decode (M <= 32) on the widest projections: 32 KB of weights per stage.
 struct GemmCfg {
   int bm, bn, wm, wn, st, bk;
 };
@@ -543,7 +545,8 @@ constexpr GemmCfg kGemmCfgs[] = {{256, 256, 2, 2, 2, 64}, {256, 128, 2, 2, 3, 64
                                  {64, 128, 2, 2, 4, 64},  {128, 128, 2, 2, 2, 64}, {64, 64, 2, 2, 4, 64},
                                  {32, 128, 1, 4, 4, 64},  {128, 64, 2, 2, 4, 64},  {256, 256, 2, 4, 2, 64},
                                  {256, 128, 2, 4, 3, 64}, {256, 256, 2, 4, 4, 32}, {256, 128, 2, 2, 6, 32},
-                                 {128, 256, 2, 4, 6, 32}, {128, 160, 4, 1, 4, 64}, {128, 96, 4, 1, 4, 64}};
+                                 {128, 256, 2, 4, 6, 32}, {128, 160, 4, 1, 4, 64}, {128, 96, 4, 1, 4, 64},
+                                 {32, 256, 1, 4, 4, 64}};
 constexpr int kGemmNumCfgs = sizeof(kGemmCfgs) / sizeof(kGemmCfgs[0]);
 // A config exists for a weight format when its A and W tiles split into whole 1 KB DMA
 // instructions per wave (int8 W rows are half as wide: 128 x 160 and 128 x 96 are fp16 only).
@@ -610,11 +613,11 @@ int gemm_blocks_per_cu(int cfg, bool q8);
     HI_GEMM_CFG(0, false) HI_GEMM_CFG(1, false) HI_GEMM_CFG(2, false) HI_GEMM_CFG(3, false)                    \
     HI_GEMM_CFG(4, false) HI_GEMM_CFG(5, false) HI_GEMM_CFG(6, false) HI_GEMM_CFG(7, false)                    \
     HI_GEMM_CFG(8, false) HI_GEMM_CFG(9, false) HI_GEMM_CFG(10, false) HI_GEMM_CFG(11, false)                  \
-    HI_GEMM_CFG(12, false) HI_GEMM_CFG(13, false) HI_GEMM_CFG(14, false)                                       \
+    HI_GEMM_CFG(12, false) HI_GEMM_CFG(13, false) HI_GEMM_CFG(14, false) HI_GEMM_CFG(15, false)                \
     HI_GEMM_CFG(0, true) HI_GEMM_CFG(1, true) HI_GEMM_CFG(2, true) HI_GEMM_CFG(3, true)                        \
     HI_GEMM_CFG(4, true) HI_GEMM_CFG(5, true) HI_GEMM_CFG(6, true) HI_GEMM_CFG(7, true)                        \
     HI_GEMM_CFG(8, true) HI_GEMM_CFG(9, true) HI_GEMM_CFG(10, true) HI_GEMM_CFG(11, true) HI_GEMM_CFG(12, true) \
-    HI_GEMM_CFG(13, true) HI_GEMM_CFG(14, true)                                                                \
+    HI_GEMM_CFG(13, true) HI_GEMM_CFG(14, true) HI_GEMM_CFG(15, true)                                          \
     HI_FAIL("gemm: no kernel for config %d", cfg);                                                             \
   }                                                                                                            \
   template <>                                                                                                  \
@@ -622,6 +625,6 @@ int gemm_blocks_per_cu(int cfg, bool q8);
     constexpr int EPI = EPIV;                                                                                  \
     HI_GEMM_OCC(0) HI_GEMM_OCC(1) HI_GEMM_OCC(2) HI_GEMM_OCC(3) HI_GEMM_OCC(4) HI_GEMM_OCC(5) HI_GEMM_OCC(6)    \
     HI_GEMM_OCC(7) HI_GEMM_OCC(8) HI_GEMM_OCC(9) HI_GEMM_OCC(10) HI_GEMM_OCC(11) HI_GEMM_OCC(12)              \
-    HI_GEMM_OCC(13) HI_GEMM_OCC(14)                                                                            \
+    HI_GEMM_OCC(13) HI_GEMM_OCC(14) HI_GEMM_OCC(15)                                                            \
     return -1;                                                                                                 \
   }

@@ -49,7 +49,8 @@ int cfg_blocks_per_cu(int cfg, bool q8) {
 }
 
 // Relative MFMA efficiency of each tile shape (bigger tiles reuse more of what they stage).
-constexpr double kCfgEff[kGemmNumCfgs] = {0.9, 0.85, 0.85, 0.6, 0.8, 0.45, 0.4, 0.6, 1.0, 0.9, 1.05, 0.85, 0.95, 0.85, 0.8};
+constexpr double kCfgEff[kGemmNumCfgs] = {0.9, 0.85, 0.85, 0.6, 0.8, 0.45, 0.4, 0.6,
+                                           1.0, 0.9, 1.05, 0.85, 0.95, 0.85, 0.8, 0.5};
 
 struct Choice {
   int cfg, splits;

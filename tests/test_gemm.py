@@ -8,7 +8,10 @@ short K (one and two K tiles per split), every epilogue, the partial SwiGLU tile
 row, int8 weights (the oracle computes on fp16(q * s)), and a captured split-K GEMM replayed after
 the workspace grew. Large shapes are checked on sampled rows (rows are computed independently, so
 the oracle's GEMM of those rows is the exact reference for them). Adds bitwise determinism of
-split-K (partials are summed in split order whatever the arrival order).
+split-K (partials are summed in split order whatever the arrival order), and the batched-decode
+tiles (M <= 64, deep rings; the role of the reference's skinny kernel, kernels.cuh:896-1115) at
+every M class, epilogue, weight format and split count, including a K tail of 32, a half-filled
+last column tile, and graph replays.
 """
 import numpy as np
 import pytest
@@ -56,7 +59,7 @@ def gemm_check(hi, O, name, A, W, r, epi=0, bias=None, scales=None, res=None, to
 
 
 # every tile configuration (the automatic choice is -1); configs past the library's count skip
-CFGS = [-1] + list(range(15))
+CFGS = [-1] + list(range(16))
 
 
 def need_cfg(hi, cfg):
@@ -102,6 +105,36 @@ def test_gemm_configs(hi, O, cfg):
         hi.lib.hi_gemm_force_config(-1)
 
 
+@pytest.mark.parametrize("cfg", CFGS)
+def test_gemm_writes_nothing_past_n(hi, O, cfg):
+    """N % 32 == 16 (allowed: N % 16 == 0): the last 32-column MFMA tile ends 16 columns past N.
+    With padded rows (ldc = N + 16) the padding and a sentinel row past M must keep their values,
+    for the store, bias and residual epilogues, one split and four."""
+    need_cfg(hi, cfg)
+    r = rng(370 + cfg)
+    hi.lib.hi_gemm_force_config(cfg)
+    try:
+        for M, N, K, epi, sp in [(5, 1552, 992, 0, 1), (70, 1040, 1024, 1, 1), (33, 1552, 1024, 0, 4),
+                                 (5, 528, 2048, 1, 4)]:
+            hi.lib.hi_gemm_force_splits(sp)
+            A = h16(r, M, K)
+            W = h16(r, N, K, sd=0.02)
+            b = h16(r, N) if epi == 0 else None
+            buf = np.full((M + 1, N + 16), 7.0, np.float16)
+            res = h16(r, M, N)
+            if epi == 1:
+                buf[:M, :N] = res
+            bd = cuda(buf)
+            hi.gemm(cuda(A), cuda(W), out=bd[:M, :N], epi=epi, bias=None if b is None else cuda(b))
+            got = host(bd)
+            ref = O.gemm(A, W, epi=epi, bias=b, out=res.copy() if epi == 1 else None)
+            check(f"cfg={cfg} M={M} N={N} epi={epi} split={sp}", got[:M, :N], ref, 4e-3, 3e-3)
+            assert (got[:, N:] == 7.0).all() and (got[M] == 7.0).all(), f"cfg={cfg} N={N}: wrote past column N or row M"
+    finally:
+        hi.lib.hi_gemm_force_config(-1)
+        hi.lib.hi_gemm_force_splits(-1)
+
+
 def test_gemm_large_prefill_shapes(hi, O):
     """Llama-3.2-3B prefill shapes at M = 2000 (non-tile-multiple), automatic choice."""
     r = rng(310)
@@ -138,7 +171,7 @@ def test_gemm_short_k(hi, O):
     tiles leaves no empty split."""
     r = rng(330)
     try:
-        for cfg in [-1, 0, 1, 5, 6, 10, 12, 13, 14]:
+        for cfg in [-1, 0, 1, 5, 6, 10, 12, 13, 14, 15]:
             hi.lib.hi_gemm_force_config(cfg)
             for sp in [1, 2]:
                 hi.lib.hi_gemm_force_splits(sp)
@@ -231,6 +264,81 @@ def test_gemm_graph_after_workspace_growth(hi, O):
         del junk
     finally:
         hi.lib.hi_gemm_force_splits(-1)
+
+
+SMALL_M = [3, 5, 6, 15]
+# (M, N, K, epi, splits): M classes 1..32 and 33..64, K tails of 32 (K = 992, 1504), a last column
+# tile partly past N, SwiGLU
+SKINNY_CASES = [(1, 2048, 1024, 0, 1), (9, 1536, 2048, 1, 2), (16, 2560, 2048, 2, 4), (17, 4096, 1024, 0, 8),
+                (32, 1024, 4096, 2, 2), (33, 2048, 1504, 1, 1), (50, 1024, 3072, 0, 4), (64, 4096, 1024, 2, 8),
+                (64, 1552, 992, 1, 2), (5, 1552, 992, 0, 8), (64, 512, 256, 0, 1)]
+
+
+@pytest.mark.parametrize("q8", [False, True], ids=["fp16", "int8"])
+@pytest.mark.parametrize("cfg", SMALL_M)
+def test_gemm_small_m(hi, O, cfg, q8):
+    need_cfg(hi, cfg)
+    r = rng(900 + cfg + 10 * q8)
+    hi.lib.hi_gemm_force_config(cfg)
+    try:
+        for M, N, K, epi, sp in SKINNY_CASES:
+            hi.lib.hi_gemm_force_splits(sp)
+            A = h16(r, M, K)
+            W = h16(r, N, K, sd=0.02) if epi != 2 else interleave(h16(r, N // 2, K, sd=0.02), h16(r, N // 2, K, sd=0.02))
+            q, s = O.quantize_rows(W) if q8 else (W, None)
+            bias = h16(r, N) if epi == 0 and M % 2 else None
+            res = h16(r, M, N) if epi == 1 else None
+            tol = (4e-3, 4e-3) if epi == 2 else (4e-3, 2e-3) if epi == 1 else (3e-3, 3e-3)
+            gemm_check(hi, O, f"small-M cfg={cfg} {'int8' if q8 else 'fp16'} M={M} N={N} K={K} epi={epi} split={sp}",
+                       A, q, r, epi=epi, bias=bias, scales=s, res=res, tol=tol)
+    finally:
+        hi.lib.hi_gemm_force_config(-1)
+        hi.lib.hi_gemm_force_splits(-1)
+
+
+def test_gemm_small_m_deterministic_and_graph(hi, O):
+    """Splits summed in split order: bit-identical across runs; a captured split launch replays
+    correctly, with eager split launches of another shape between the replays."""
+    import torch
+    r = rng(950)
+    hi.lib.hi_gemm_force_config(6)
+    hi.lib.hi_gemm_force_splits(8)
+    try:
+        xh, Wh = h16(r, 40, 4096), h16(r, 3072, 4096, sd=0.02)
+        x, W = cuda(xh), cuda(Wh)
+        a = host(hi.gemm(x, W))
+        for _ in range(3):
+            assert np.array_equal(bits(host(hi.gemm(x, W))), bits(a))
+        check("small-M split 8", a, O.gemm(xh, Wh), 3e-3, 3e-3)
+        out = torch.empty(40, 3072, dtype=torch.float16, device="cuda")
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            hi.gemm(x, W, out=out)
+        x2h, W2h = h16(r, 7, 2048), h16(r, 6144, 2048, sd=0.02)
+        x2, W2 = cuda(x2h), cuda(W2h)
+        ref2 = O.gemm(x2h, W2h)
+        for _ in range(3):
+            out.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(host(out)), bits(a)), "graph replay differs from the eager result"
+            check("small-M eager between replays", host(hi.gemm(x2, W2)), ref2, 3e-3, 3e-3)
+    finally:
+        hi.lib.hi_gemm_force_config(-1)
+        hi.lib.hi_gemm_force_splits(-1)
+
+
+def test_gemm_small_m_automatic(hi, O):
+    """The automatic choice at decode batch sizes (Llama-3.1-8B projections)."""
+    r = rng(960)
+    for M in [9, 24, 40, 64]:
+        for N, K, epi in [(6144, 4096, 0), (4096, 4096, 1), (28672, 4096, 2), (4096, 14336, 1)]:
+            A = h16(r, M, K)
+            W = h16(r, N, K, sd=0.02)
+            res = h16(r, M, N) if epi == 1 else None
+            gemm_check(hi, O, f"auto M={M} N={N} K={K} epi={epi}", A, W, r, epi=epi, res=res,
+                       tol=(4e-3, 4e-3) if epi == 2 else (4e-3, 2e-3))
 
 
 def test_gemm_rejects_bad_shapes(hi):
