@@ -46,6 +46,9 @@ _OPTIONAL = {
     "hi_decode_attn": [P, I, P, P, I, P, P, I, I, I, I, I, P, P],
     "hi_argmax": [P, I, I, P, P],
     "hi_embed": [P, P, I, I, P, I, I, P],
+    "hi_rope_cache": [P, I, I, I, I, I, P, P, I, I, P, P, I, P],
+    "hi_flash_prefill": [P, I, P, P, I, P, I, I, I, I, I, I, P],
+    "hi_flash_prefill_lse": [P, I, P, P, I, P, I, I, I, I, I, I, P, P],
 }
 for _name, _args in list(_SIGS.items()) + [(n, a) for n, a in _OPTIONAL.items() if hasattr(lib, n)]:
     _fn = getattr(lib, _name)
@@ -177,6 +180,44 @@ def decode_attn(q, kc, vc, pos, Hq, Hkv, out=None, work=None):
     _ok(lib.hi_decode_attn(_p(q), q.stride(0), _p(kc), _p(vc), kc.shape[2], _p(pos), _p(out), out.stride(0), B, Hq, Hkv, D,
                            _p(work), _s()), "decode_attn")
     return out
+
+
+def rope_cache(qkv, Hq, Hkv, cs, kc, vc, pos=None, pos_base=0, slot_base=0):
+    """RoPE + KV-cache write after a QKV GEMM (reference scripts/hipinfer.py:164-168): qkv [M,
+    (Hq+2Hkv)*D] gets its q heads rotated in place; the rotated k and raw v rows go to kc/vc
+    [slots, Hkv, max_seq, D]; cs [max_seq, D/2, 2] fp16. Row m sits at pos[m] in slot
+    slot_base + m (decode), or at pos_base + m in slot slot_base (prefill)."""
+    D = kc.shape[-1]
+    _dev(qkv, cs, kc, vc, pos)
+    _ok(lib.hi_rope_cache(_p(qkv), qkv.stride(0), qkv.shape[0], Hq, Hkv, D, _p(cs), _p(pos), pos_base, slot_base,
+                          _p(kc), _p(vc), kc.shape[2], _s()), "rope_cache")
+
+
+def flash_prefill(q, kc, vc, T, p0, Hq, Hkv, out=None):
+    """Causal prefill attention (reference scripts/hipinfer.py:171-177): q [T, ldq] with head h at
+    columns h*D, row t at position p0 + t; kc/vc [Hkv, max_seq, D] of one cache slot. Returns out
+    [T, Hq*D] fp16."""
+    D = kc.shape[-1]
+    if out is None:
+        out = torch.empty(T, Hq * D, dtype=torch.float16, device=q.device)
+    _dev(q, kc, vc, out)
+    _ok(lib.hi_flash_prefill(_p(q), q.stride(0), _p(kc), _p(vc), kc.shape[1], _p(out), out.stride(0), T, p0, Hq, Hkv,
+                             D, _s()), "flash_prefill")
+    return out
+
+
+def flash_prefill_lse(q, kc, vc, T, p0, Hq, Hkv, out=None, lse=None):
+    """flash_prefill that also returns each row's log2-domain log-sum-exp, lse [Hq, T] fp32
+    (reference scripts/hipinfer.py:193-202)."""
+    D = kc.shape[-1]
+    if out is None:
+        out = torch.empty(T, Hq * D, dtype=torch.float16, device=q.device)
+    if lse is None:
+        lse = torch.empty(Hq, T, dtype=torch.float32, device=q.device)
+    _dev(q, kc, vc, out, lse)
+    _ok(lib.hi_flash_prefill_lse(_p(q), q.stride(0), _p(kc), _p(vc), kc.shape[1], _p(out), out.stride(0), T, p0, Hq,
+                                 Hkv, D, _p(lse), _s()), "flash_prefill_lse")
+    return out, lse
 
 
 def argmax(logits, out=None):

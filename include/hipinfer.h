@@ -102,6 +102,24 @@ int hi_argmax(const void* logits, int B, int V, int* tok_out, void* stream);
  * caller can build the whole decode step from C-ABI calls. */
 int hi_embed(const int* tok, const void* table, int V, int H, void* x, int ldx, int B, void* stream);
 
+/* ---- prefill kernels around the GEMM
+ * RoPE + KV-cache write of M qkv rows [M, ldq] = [q (Hq*D) | k (Hkv*D) | v (Hkv*D)]: q rotated in
+ * place (HF order, per-op fp16 rounding), rotated k and raw v to kc / vc [slots][Hkv][max_seq][D].
+ * Row m sits at pos[m] in slot slot_base + m (pos non-null), else at pos_base + m in slot slot_base.
+ * cs [max_seq][D/2] (cos, sin) fp16. Replaces api.cu:584-586 (hi_rope_cache); hipinfer.py:164-168. */
+int hi_rope_cache(void* qkv, int ldq, int M, int Hq, int Hkv, int D, const void* cs, const int* pos, int pos_base,
+                  int slot_base, void* kc, void* vc, int max_seq, void* stream);
+/* Causal prefill attention: row t of q [T, ldq] (head h at columns h*D) sits at position p0 + t and
+ * attends to keys 0..p0+t of one cache slot kc / vc [Hkv][max_seq][D] (kv head h / (Hq / Hkv));
+ * out [T, ldo] fp16. D 64 or 128, p0 + T <= max_seq. Replaces api.cu:614-617 (hi_flash_prefill);
+ * hipinfer.py:171-177. */
+int hi_flash_prefill(const void* q, int ldq, const void* kc, const void* vc, int max_seq, void* out, int ldo, int T,
+                     int p0, int Hq, int Hkv, int D, void* stream);
+/* The same, and each row's log2-domain log-sum-exp of the scaled logits into lse [Hq][T] fp32.
+ * Replaces api.cu:619-623 (hi_flash_prefill_lse); hipinfer.py:193-202. */
+int hi_flash_prefill_lse(const void* q, int ldq, const void* kc, const void* vc, int max_seq, void* out, int ldo,
+                         int T, int p0, int Hq, int Hkv, int D, float* lse, void* stream);
+
 /* ---- RMSNorm (unfused form of the GEMV prologue; the reference's tests build references with it)
  * y[M, H] = w * fp16(x * rsqrt(mean(x^2) + eps)), rows contiguous. Replaces api.cu:76-79
  * (hi_rmsnorm); hipinfer.py:13. */

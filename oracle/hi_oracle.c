@@ -22,6 +22,11 @@
  *   or_decode_attn      src/kernels.cuh:1486-1660 (decode_attn_kernel), api.cu:694-720;
  *                       CPU reference form tests/test_kernels.py:298-307 (ref_attn)
  *   or_argmax           src/kernels.cuh:1883-1931 (argmax_better, block_argmax, argmax_kernel)
+ *   or_rope_cache       src/kernels.cuh:1120-1158 (rope_cache_kernel), api.cu:579-586;
+ *                       CPU reference form tests/test_kernels.py:230-261 (hf_rope)
+ *   or_flash_prefill    src/kernels.cuh:1160-1329 (flash_prefill_kernel), api.cu:594-623;
+ *                       CPU reference form tests/test_kernels.py:288-309 (ref_attn, causal on
+ *                       absolute positions p0 + t)
  *
  * fp16 conversions are this file's own IEEE binary16 routines (round to nearest even, subnormals,
  * overflow to inf). Accumulation is fp64; the reference accumulates in fp32 in kernel-specific
@@ -463,6 +468,72 @@ int or_argmax(const uint16_t* logits, int B, int V, int32_t* tok) {
       }
     }
     tok[b] = bi;
+  }
+  return 0;
+}
+
+/* RoPE of the q and k heads of each qkv row and the KV-cache write (src/kernels.cuh:1120-1158):
+ * row m sits at position pos[m] in slot slot_base + m (decode form, pos non-null) or at position
+ * pos_base + m in slot slot_base (prefill form). q heads are rotated in place; rotated k heads and
+ * the raw v heads go to cache [slot][Hkv][max_seq][D]. */
+int or_rope_cache(uint16_t* qkv, int64_t ldq, int M, int Hq, int Hkv, int D, const uint16_t* cs, const int32_t* pos,
+                  int pos_base, int slot_base, uint16_t* kc, uint16_t* vc, int max_seq) {
+  if (M < 0 || Hq < 1 || Hkv < 1 || D < 2 || D % 2 || max_seq < 1) return -1;
+  const int HD = D / 2;
+  for (int m = 0; m < M; m++) {
+    const int p = pos ? pos[m] : pos_base + m, slot = pos ? slot_base + m : slot_base;
+    if (p < 0 || p >= max_seq || slot < 0) return -1;
+    uint16_t* row = qkv + (int64_t)m * ldq;
+    for (int head = 0; head < Hq + Hkv; head++)
+      for (int d = 0; d < HD; d++) {
+        uint16_t* x = row + (int64_t)head * D;
+        const uint16_t* t = cs + ((int64_t)p * HD + d) * 2;
+        uint16_t y1, y2;
+        or_rope_pair(x[d], x[d + HD], t[0], t[1], &y1, &y2);
+        uint16_t* dst = head < Hq ? x : kc + (((int64_t)slot * Hkv + head - Hq) * max_seq + p) * D;
+        dst[d] = y1;
+        dst[d + HD] = y2;
+      }
+    for (int i = 0; i < Hkv * D; i++)
+      vc[(((int64_t)slot * Hkv + i / D) * max_seq + p) * D + i % D] = row[(int64_t)(Hq + Hkv) * D + i];
+  }
+  return 0;
+}
+
+/* Causal prefill attention over a cache slot (src/kernels.cuh:1160-1329): query row t (head h at
+ * columns h*D of q) sits at position p0 + t and attends to keys 0..p0+t of kv head h / (Hq/Hkv),
+ * softmax(q.k / sqrt(D)) v in fp64, one rounding to fp16. lse (optional, [Hq][T] fp32) is each
+ * row's log-sum-exp in the log2 domain of the scaled logits, log2(sum_j 2^(s_j log2(e)/sqrt(D))). */
+int or_flash_prefill(const uint16_t* q, int64_t ldq, const uint16_t* kc, const uint16_t* vc, int max_seq,
+                     uint16_t* out, int64_t ldo, int T, int p0, int Hq, int Hkv, int D, float* lse) {
+  if (T < 0 || p0 < 0 || p0 + T > max_seq || Hkv < 1 || Hq < Hkv || Hq % Hkv || D < 1) return -1;
+  const int G = Hq / Hkv;
+#pragma omp parallel for schedule(dynamic)
+  for (int th = 0; th < T * Hq; th++) {
+    const int t = th / Hq, h = th % Hq, L = p0 + t + 1;
+    const uint16_t* qh = q + (int64_t)t * ldq + (int64_t)h * D;
+    const uint16_t* K = kc + (int64_t)(h / G) * max_seq * D;
+    const uint16_t* V = vc + (int64_t)(h / G) * max_seq * D;
+    double* s = (double*)malloc((size_t)L * sizeof(double));
+    double mx = -INFINITY;
+    for (int j = 0; j < L; j++) {
+      double acc = 0.0;
+      for (int d = 0; d < D; d++) acc += (double)or_h2f(qh[d]) * (double)or_h2f(K[(int64_t)j * D + d]);
+      s[j] = acc / sqrt((double)D);
+      if (s[j] > mx) mx = s[j];
+    }
+    double den = 0.0;
+    for (int j = 0; j < L; j++) {
+      s[j] = exp(s[j] - mx);
+      den += s[j];
+    }
+    for (int d = 0; d < D; d++) {
+      double o = 0.0;
+      for (int j = 0; j < L; j++) o += s[j] * (double)or_h2f(V[(int64_t)j * D + d]);
+      out[(int64_t)t * ldo + (int64_t)h * D + d] = or_f2h((float)(o / den));
+    }
+    if (lse) lse[(int64_t)h * T + t] = (float)((mx + log(den)) / log(2.0));
+    free(s);
   }
   return 0;
 }

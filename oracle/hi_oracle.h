@@ -51,6 +51,10 @@ int or_moe_experts(const uint16_t* xn, int64_t ldxn, const uint16_t* wgu, const 
 int or_decode_attn(const uint16_t* q, int64_t ldq, const uint16_t* kc, const uint16_t* vc, int max_seq,
                    const int32_t* pos, uint16_t* out, int64_t ldo, int B, int Hq, int Hkv, int D);
 int or_argmax(const uint16_t* logits, int B, int V, int32_t* tok);
+int or_rope_cache(uint16_t* qkv, int64_t ldq, int M, int Hq, int Hkv, int D, const uint16_t* cs, const int32_t* pos,
+                  int pos_base, int slot_base, uint16_t* kc, uint16_t* vc, int max_seq);
+int or_flash_prefill(const uint16_t* q, int64_t ldq, const uint16_t* kc, const uint16_t* vc, int max_seq,
+                     uint16_t* out, int64_t ldo, int T, int p0, int Hq, int Hkv, int D, float* lse);
 
 #ifdef __cplusplus
 }

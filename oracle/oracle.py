@@ -43,6 +43,8 @@ def _load():
         "or_moe_experts": ([P, I64, P, P, P, P, I, I, I, I, I, I, F, P, I64], I),
         "or_decode_attn": ([P, I64, P, P, I, P, P, I64, I, I, I, I], I),
         "or_argmax": ([P, I, I, P], I),
+        "or_rope_cache": ([P, I64, I, I, I, I, P, P, I, I, P, P, I], I),
+        "or_flash_prefill": ([P, I64, P, P, I, P, I64, I, I, I, I, I, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -239,3 +241,32 @@ def argmax(logits):
     tok = np.empty(B, np.int32)
     _ok(lib.or_argmax(_p(logits), B, V, _p(tok)), "argmax")
     return tok
+
+
+def rope_cache(qkv, Hq, Hkv, cs, kc, vc, pos=None, pos_base=0, slot_base=0):
+    """RoPE + KV-cache write (src/kernels.cuh:1120-1158), in place like the reference: qkv [M,
+    (Hq+2Hkv)*D] gets its q heads rotated; kc/vc [slots, Hkv, max_seq, D] get the rotated k and raw v
+    rows; cs [max_seq, D/2, 2] fp16. Returns (qkv, kc, vc)."""
+    for a in (qkv, kc, vc):
+        assert a.flags.c_contiguous and a.dtype == np.float16
+    cs = _c(cs, np.float16)
+    M = qkv.shape[0]
+    D = kc.shape[-1]
+    pp = None if pos is None else _c(pos, np.int32)
+    _ok(lib.or_rope_cache(_p(qkv), qkv.shape[1], M, Hq, Hkv, D, _p(cs), None if pp is None else _p(pp), pos_base,
+                          slot_base, _p(kc), _p(vc), kc.shape[2]), "rope_cache")
+    return qkv, kc, vc
+
+
+def flash_prefill(q, kc, vc, T, p0, Hq, Hkv, lse=False):
+    """Causal prefill attention (src/kernels.cuh:1160-1329; tests/test_kernels.py:288-309): q [T,
+    Hq*D] (head h at columns h*D), kc/vc [Hkv, max_seq, D] of one slot, row t at position p0 + t.
+    Returns out [T, Hq*D] fp16 (and lse [Hq, T] fp32, log2 domain, when lse=True)."""
+    q, kc, vc = _c(q, np.float16), _c(kc, np.float16), _c(vc, np.float16)
+    Hkv_, S, D = kc.shape
+    assert Hkv_ == Hkv
+    out = np.empty((T, Hq * D), np.float16)
+    ls = np.empty((Hq, T), np.float32) if lse else None
+    _ok(lib.or_flash_prefill(_p(q), q.shape[1], _p(kc), _p(vc), S, _p(out), Hq * D, T, p0, Hq, Hkv, D,
+                             None if ls is None else _p(ls)), "flash_prefill")
+    return (out, ls) if lse else out

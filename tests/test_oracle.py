@@ -416,3 +416,94 @@ def test_argmax_matches_numpy_and_edge_rows():
     got = O.argmax(lg)
     assert np.array_equal(got, np.argmax(lg, -1).astype(np.int32)), got
     assert list(got[[1, 3, 4, 6, 7]]) == [100, 0, 0, 12, 0]
+
+
+# ------------------------------------------------------------------ prefill: rope_cache, flash_prefill
+def test_rope_cache_matches_golden_pinned_qkv_rope():
+    """rope_cache on a qkv row equals gemv_qkv_rope (pinned bit for bit by the golden vectors above)
+    with identity weights, whose projection is the row itself (one exact product per output), in
+    both the decode form (per-row positions and slots) and the prefill form (pos_base + m in one
+    slot); v is copied, never rotated."""
+    r = np.random.default_rng(40)
+    for Hq, Hkv, D in [(4, 2, 64), (3, 1, 128)]:
+        S, M = 300, 3
+        nh = Hq + 2 * Hkv
+        ang = np.arange(S)[:, None] * (1.0 / 10000.0 ** (np.arange(0, D, 2) / D))[None, :]
+        cs = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float16)
+        x = r.standard_normal((M, nh * D)).astype(np.float16)
+        eye = np.eye(nh * D, dtype=np.float16)
+        pos = np.array([7, 299, 0], np.int32)
+        out = np.zeros((M, Hq * D), np.float16)
+        kc_ref = np.zeros((M, Hkv, S, D), np.float16)
+        vc_ref = np.zeros_like(kc_ref)
+        O.gemv_qkv_rope(x, eye, None, Hq, Hkv, cs, pos, kc_ref, vc_ref, out)
+        qkv = x.copy()
+        kc, vc = np.zeros_like(kc_ref), np.zeros_like(vc_ref)
+        O.rope_cache(qkv, Hq, Hkv, cs, kc, vc, pos=pos)
+        assert np.array_equal(bits(qkv[:, :Hq * D]), bits(out))
+        assert np.array_equal(bits(qkv[:, Hq * D:]), bits(x[:, Hq * D:])), "k/v columns must stay as they were"
+        assert np.array_equal(bits(kc), bits(kc_ref)) and np.array_equal(bits(vc), bits(vc_ref))
+        # prefill form: rows at positions p0..p0+M-1 of slot 1
+        p0 = 100
+        qkv = x.copy()
+        kc, vc = np.zeros((2, Hkv, S, D), np.float16), np.zeros((2, Hkv, S, D), np.float16)
+        O.rope_cache(qkv, Hq, Hkv, cs, kc, vc, pos_base=p0, slot_base=1)
+        for m in range(M):
+            o1 = np.zeros((1, Hq * D), np.float16)
+            k1, v1 = np.zeros((1, Hkv, S, D), np.float16), np.zeros((1, Hkv, S, D), np.float16)
+            O.gemv_qkv_rope(x[m:m + 1], eye, None, Hq, Hkv, cs, np.array([p0 + m], np.int32), k1, v1, o1)
+            assert np.array_equal(bits(qkv[m, :Hq * D]), bits(o1[0]))
+            assert np.array_equal(bits(kc[1, :, p0 + m]), bits(k1[0, :, p0 + m]))
+            assert np.array_equal(bits(vc[1, :, p0 + m]), bits(v1[0, :, p0 + m]))
+        assert not kc[0].any() and not vc[0].any(), "slot 0 untouched"
+
+
+def test_flash_prefill_rows_are_decode_attention():
+    """Row t of a prefill is decode attention at position p0 + t over the same slot (decode_attn is
+    pinned by closed forms and numpy above), bit for bit; T = 1 at p0 = 0 returns the first value
+    row; a zero query gives the prefix mean; lse of a zero query is log2 of the key count."""
+    r = np.random.default_rng(41)
+    for Hq, Hkv, D, T, p0 in [(8, 2, 64, 37, 0), (6, 6, 128, 20, 50), (7, 1, 128, 5, 300)]:
+        S = p0 + T + 3
+        q = r.standard_normal((T, Hq * D)).astype(np.float16)
+        kc = r.standard_normal((Hkv, S, D)).astype(np.float16)
+        vc = r.standard_normal((Hkv, S, D)).astype(np.float16)
+        got, lse = O.flash_prefill(q, kc, vc, T, p0, Hq, Hkv, lse=True)
+        dec = O.decode_attn(q, np.broadcast_to(kc, (T,) + kc.shape).copy(), np.broadcast_to(vc, (T,) + vc.shape).copy(),
+                            np.arange(p0, p0 + T, dtype=np.int32), Hq, Hkv)
+        assert np.array_equal(bits(got), bits(dec)), (Hq, Hkv, D, T, p0)
+        # lse against numpy: log2 sum 2^(s log2 e / sqrt D)
+        G = Hq // Hkv
+        for t in [0, T - 1]:
+            for h in [0, Hq - 1]:
+                s = kc[h // G, :p0 + t + 1].astype(np.float64) @ q[t, h * D:(h + 1) * D].astype(np.float64) / np.sqrt(D)
+                ref = np.log2(np.exp(s - s.max()).sum()) + s.max() / np.log(2)
+                assert abs(lse[h, t] - ref) <= 1e-5 * max(1.0, abs(ref)), (t, h, lse[h, t], ref)
+        z, lz = O.flash_prefill(np.zeros_like(q), kc, vc, T, p0, Hq, Hkv, lse=True)
+        for t in [0, T // 2, T - 1]:
+            mean = vc[:, :p0 + t + 1].astype(np.float64).mean(1)  # [Hkv, D]
+            assert np.array_equal(z[t].reshape(Hq, D), np.repeat(mean, G, 0).astype(np.float32).astype(np.float16))
+            assert np.allclose(lz[:, t], np.log2(p0 + t + 1), rtol=0, atol=1e-6)
+    one = O.flash_prefill(q[:1], kc, vc, 1, 0, Hq, Hkv)
+    assert np.array_equal(one.reshape(Hq, -1), np.repeat(vc[:, 0], Hq // Hkv, 0))
+
+
+def test_flash_prefill_vs_numpy_float64_causal():
+    """Against a float64 numpy restatement of the reference's ref_attn (tests/test_kernels.py:288-296):
+    softmax over the causal mask key <= p0 + t."""
+    r = np.random.default_rng(42)
+    Hq, Hkv, D, T, p0 = 4, 2, 64, 29, 13
+    S = 64
+    q = r.standard_normal((T, Hq * D)).astype(np.float16)
+    kc = r.standard_normal((Hkv, S, D)).astype(np.float16)
+    vc = r.standard_normal((Hkv, S, D)).astype(np.float16)
+    got = O.flash_prefill(q, kc, vc, T, p0, Hq, Hkv).astype(np.float64)
+    G = Hq // Hkv
+    k = np.repeat(kc[:, :p0 + T].astype(np.float64), G, 0)
+    v = np.repeat(vc[:, :p0 + T].astype(np.float64), G, 0)
+    s = np.einsum("thd,hld->htl", q.astype(np.float64).reshape(T, Hq, D), k) / np.sqrt(D)
+    s[:, np.arange(p0 + T)[None, :] > (p0 + np.arange(T))[:, None]] = -np.inf
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    ref = np.einsum("htl,hld->thd", p, v).reshape(T, Hq * D)
+    assert np.all(np.abs(got - ref) <= 2.0 ** -11 * np.abs(ref) + 1e-7)
