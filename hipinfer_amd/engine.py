@@ -1,38 +1,61 @@
-"""Greedy decode step of a dense Llama-family model over weights already in device memory, built
-only from this library's C-ABI calls.
+"""Prefill and greedy decode of a dense Llama-family model over weights already in device memory,
+built only from this library's C-ABI calls.
 
-Follows the reference engine's decode_step (src/api.cu:1891-1952) on its GEMV path (batch up to 8,
-RMSNorm fused into the projections), one sequence per cache slot:
+Follows the reference engine (src/api.cu): prefill (1807-1845) and decode_step (1891-1952), one
+sequence per cache slot.
 
-    x = embed[tok]                                        (embed_kernel, api.cu:1900)
+Prefill of T prompt tokens into slot s at positions p0.. (chunks of at most max_prefill rows):
+
+    x = embed[tokens]                                     (embed_kernel, api.cu:1817)
+    per layer l (attn_rows / mlp_rows, api.cu:1668-1713):
+      qkv = RMSNorm(x; n1) @ Wqkv^T + bqkv                (hi_rmsnorm, hi_gemm epi 0)
+      q rotated, K/V[s, p0..] = RoPE(k), v                (hi_rope_cache, prefill form)
+      att = causal softmax(q K^T / sqrt(D)) V             (hi_flash_prefill over slot s)
+      x  += att @ Wo^T                                    (hi_gemm epi 1)
+      x  += SwiGLU(RMSNorm(x; n2) @ Wgu^T) @ Wdown^T      (hi_rmsnorm, hi_gemm epi 2, hi_gemm epi 1)
+    logits[s] = RMSNorm(x[T-1]; nf) @ Wlm^T               (GEMV, api.cu:1829-1836)
+    tok[s] = argmax(logits[s]); pos[s] = p0 + T
+
+Decode step for slots 0..B-1 (tok and pos live on the device and advance there, so one captured
+hipGraph replays step after step). Up to 8 sequences take the GEMV path with RMSNorm fused into
+the projections; 9 to 64 the GEMM path (api.cu:1914-1940), whose tiles are tuned by the first,
+eager step:
+
+    x = embed[tok]
     per layer l:
-      q, K/V[pos] = RoPE(RMSNorm(x; n1) @ Wqkv^T + bqkv)  (gemv_qkv_rope, 1907-1914)
-      att = softmax(q K[0..pos]^T / sqrt(D)) V            (hi_decode_attn, 1921)
-      x  += att @ Wo^T                                    (gemv epi 1, 1929)
-      act = SwiGLU(RMSNorm(x; n2) @ Wgu^T)                (gemv epi 2, 1931)
-      x  += act @ Wdown^T                                 (gemv epi 1, 1933)
-    logits = RMSNorm(x; nf) @ Wlm^T                       (1942)
-    tok = argmax(logits); pos += 1                        (greedy / emit_token, 1948, kernels.cuh:1913-1931)
+      GEMV: q, K/V[pos] = RoPE(RMSNorm(x; n1) @ Wqkv^T + bqkv)   (gemv_qkv_rope)
+      GEMM: qkv = RMSNorm(x; n1) @ Wqkv^T + bqkv; RoPE + cache   (hi_rmsnorm, hi_gemm, hi_rope_cache)
+      att = softmax(q K[0..pos]^T / sqrt(D)) V                    (hi_decode_attn)
+      x  += att @ Wo^T
+      x  += SwiGLU(RMSNorm(x; n2) @ Wgu^T) @ Wdown^T
+    logits = RMSNorm(x; nf) @ Wlm^T
+    tok = argmax(logits); pos += 1                                (greedy, kernels.cuh:1913-1931)
 
-tok and pos live on the device and advance there, so one captured hipGraph replays step after step.
-The weight-file loader and the prefill that the reference's hi_load / hi_prefill add around this
-step are not part of this package; a caller supplies the weights and fills the caches.
+The weight-file loader that the reference's hi_load adds around this is not part of this
+package; a caller supplies the weights.
 """
 import torch
 
 from . import hipinfer as hi
+
+GEMV_MAX = 8  # sequences per decode step on the GEMV path (the reference's HIPINFER_GEMV_MAX cap)
+GEMM_MAX = 64  # and on the batched-decode GEMM path
 
 
 class DecodeStep:
     """cfg: dict with hidden H, heads Hq, kv heads Hkv, head_dim D, inter I, vocab V, layers L,
     eps, rope theta. weights: {"embed": [V, H], "lm": [V, H] or (int8, scales), "nf": [H],
     "layers": [{"qkv", "o", "gate_up", "down": [N, K] fp16 or (int8, scales); "bqkv": bias or None;
-    "n1", "n2": [H]}]} with gate/up rows interleaved in groups of 16 (export.py:97-101)."""
+    "n1", "n2": [H]}]} with gate/up rows interleaved in groups of 16 (export.py:97-101).
+    B: cache slots = sequences per decode step (1..64); max_prefill: rows per prefill chunk (0: no
+    prefill buffers)."""
 
-    def __init__(self, cfg, weights, B, max_seq):
-        assert 1 <= B <= 8, "the GEMV path serves up to 8 sequences"
+    def __init__(self, cfg, weights, B, max_seq, max_prefill=0):
+        assert 1 <= B <= GEMM_MAX, f"1..{GEMM_MAX} sequences per decode step"
         self.c, self.w, self.B, self.max_seq = dict(cfg), weights, B, max_seq
+        self.gemm_path = B > GEMV_MAX
         H, Hq, Hkv, D, I, V, L = (cfg[k] for k in ("H", "Hq", "Hkv", "D", "I", "V", "L"))
+        self.qkv_dim = (Hq + 2 * Hkv) * D
         dev = "cuda"
         f16 = torch.float16
         self.x = torch.zeros(B, H, dtype=f16, device=dev)
@@ -40,6 +63,9 @@ class DecodeStep:
         self.att = torch.zeros(B, Hq * D, dtype=f16, device=dev)
         self.act = torch.zeros(B, I, dtype=f16, device=dev)
         self.logits = torch.zeros(B, V, dtype=f16, device=dev)
+        if self.gemm_path:
+            self.xn = torch.zeros(B, H, dtype=f16, device=dev)
+            self.qkv = torch.zeros(B, self.qkv_dim, dtype=f16, device=dev)
         self.kc = [torch.zeros(B, Hkv, max_seq, D, dtype=f16, device=dev) for _ in range(L)]
         self.vc = [torch.zeros_like(k) for k in self.kc]
         self.tok = torch.zeros(B, dtype=torch.int32, device=dev)
@@ -49,35 +75,101 @@ class DecodeStep:
         inv = 1.0 / theta ** (torch.arange(0, D, 2, device=dev, dtype=torch.float64) / D)
         ang = torch.arange(max_seq, device=dev, dtype=torch.float64)[:, None] * inv[None, :]
         self.cs = torch.stack([ang.cos(), ang.sin()], -1).to(f16).contiguous()  # [max_seq, D/2, 2]
+        self.max_prefill = max_prefill
+        if max_prefill:
+            P = max_prefill
+            self.px = torch.zeros(P, H, dtype=f16, device=dev)
+            self.pxn = torch.zeros(P, H, dtype=f16, device=dev)
+            self.pqkv = torch.zeros(P, self.qkv_dim, dtype=f16, device=dev)
+            self.patt = torch.zeros(P, Hq * D, dtype=f16, device=dev)
+            self.pact = torch.zeros(P, I, dtype=f16, device=dev)
+            self.ptok = torch.zeros(P, dtype=torch.int32, device=dev)
 
     @staticmethod
     def _ws(W):
         return (W[0], W[1]) if isinstance(W, tuple) else (W, None)
 
+    def _mlp_gemm(self, ly, x, xn, act, eps):
+        """x += SwiGLU(RMSNorm(x; n2) @ Wgu^T) @ Wdown^T on the GEMM (rows of x)."""
+        hi.rmsnorm(x, ly["n2"], eps, out=xn)
+        Wg, sg = self._ws(ly["gate_up"])
+        hi.gemm(xn, Wg, out=act, epi=2, scales=sg)
+        Wd, sd = self._ws(ly["down"])
+        hi.gemm(act, Wd, out=x, epi=1, scales=sd)
+
     def step(self):
         """One token for every slot: reads tok / pos, writes the next tok, advances pos."""
         c, w = self.c, self.w
         eps = float(c.get("eps", 1e-5))
+        Hq, Hkv, D = c["Hq"], c["Hkv"], c["D"]
         hi.embed(self.tok, w["embed"], out=self.x)
         for l, ly in enumerate(w["layers"]):
             Wq, sq = self._ws(ly["qkv"])
-            hi.gemv_qkv_rope(self.x, Wq, ly["n1"], c["Hq"], c["Hkv"], self.cs, self.pos, self.kc[l], self.vc[l], self.q,
-                             bias=ly.get("bqkv"), eps=eps, scales=sq)
-            hi.decode_attn(self.q, self.kc[l], self.vc[l], self.pos, c["Hq"], c["Hkv"], out=self.att, work=self.work)
+            if self.gemm_path:
+                hi.rmsnorm(self.x, ly["n1"], eps, out=self.xn)
+                hi.gemm(self.xn, Wq, out=self.qkv, bias=ly.get("bqkv"), scales=sq)
+                hi.rope_cache(self.qkv, Hq, Hkv, self.cs, self.kc[l], self.vc[l], pos=self.pos)
+                q = self.qkv[:, :Hq * D]
+            else:
+                hi.gemv_qkv_rope(self.x, Wq, ly["n1"], Hq, Hkv, self.cs, self.pos, self.kc[l], self.vc[l], self.q,
+                                 bias=ly.get("bqkv"), eps=eps, scales=sq)
+                q = self.q
+            hi.decode_attn(q, self.kc[l], self.vc[l], self.pos, Hq, Hkv, out=self.att, work=self.work)
             Wo, so = self._ws(ly["o"])
-            hi.gemv(self.att, Wo, out=self.x, epi=1, scales=so)
-            Wg, sg = self._ws(ly["gate_up"])
-            hi.gemv(self.x, Wg, out=self.act, normw=ly["n2"], eps=eps, epi=2, scales=sg)
-            Wd, sd = self._ws(ly["down"])
-            hi.gemv(self.act, Wd, out=self.x, epi=1, scales=sd)
+            if self.gemm_path:
+                hi.gemm(self.att, Wo, out=self.x, epi=1, scales=so)
+                self._mlp_gemm(ly, self.x, self.xn, self.act, eps)
+            else:
+                hi.gemv(self.att, Wo, out=self.x, epi=1, scales=so)
+                Wg, sg = self._ws(ly["gate_up"])
+                hi.gemv(self.x, Wg, out=self.act, normw=ly["n2"], eps=eps, epi=2, scales=sg)
+                Wd, sd = self._ws(ly["down"])
+                hi.gemv(self.act, Wd, out=self.x, epi=1, scales=sd)
         Wl, sl = self._ws(w["lm"])
-        hi.gemv(self.x, Wl, out=self.logits, normw=w["nf"], eps=eps, scales=sl)
+        if self.gemm_path:
+            hi.rmsnorm(self.x, w["nf"], eps, out=self.xn)
+            hi.gemm(self.xn, Wl, out=self.logits, scales=sl)
+        else:
+            hi.gemv(self.x, Wl, out=self.logits, normw=w["nf"], eps=eps, scales=sl)
         hi.argmax(self.logits, out=self.tok)
         self.pos.add_(1)
 
     def capture(self):
-        """The step as a hipGraph (replay it to decode; tok / pos advance on the device)."""
+        """The step as a hipGraph (replay it to decode; tok / pos advance on the device). On the
+        GEMM path, run one eager step first: tile tuning does not run under capture."""
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             self.step()
         return g
+
+    def prefill(self, slot, tokens, p0=0):
+        """Prefill the prompt `tokens` (host ints) into cache slot `slot` at positions p0..; leaves the
+        last position's logits in logits[slot], the greedy next token in tok[slot] and its position
+        p0 + len(tokens) in pos[slot]. Returns that token."""
+        c, w = self.c, self.w
+        T = len(tokens)
+        assert self.max_prefill > 0, "built without prefill buffers (max_prefill=0)"
+        assert 0 <= slot < self.B and T >= 1 and 0 <= p0 and p0 + T <= self.max_seq
+        eps = float(c.get("eps", 1e-5))
+        Hq, Hkv, D = c["Hq"], c["Hkv"], c["D"]
+        toks = torch.as_tensor(list(tokens), dtype=torch.int32)
+        for t0 in range(0, T, self.max_prefill):
+            n = min(self.max_prefill, T - t0)
+            pb = p0 + t0
+            self.ptok[:n].copy_(toks[t0:t0 + n])
+            x, xn, qkv, att, act = self.px[:n], self.pxn[:n], self.pqkv[:n], self.patt[:n], self.pact[:n]
+            hi.embed(self.ptok[:n], w["embed"], out=x)
+            for l, ly in enumerate(w["layers"]):
+                hi.rmsnorm(x, ly["n1"], eps, out=xn)
+                Wq, sq = self._ws(ly["qkv"])
+                hi.gemm(xn, Wq, out=qkv, bias=ly.get("bqkv"), scales=sq)
+                hi.rope_cache(qkv, Hq, Hkv, self.cs, self.kc[l], self.vc[l], pos_base=pb, slot_base=slot)
+                hi.flash_prefill(qkv[:, :Hq * D], self.kc[l][slot], self.vc[l][slot], n, pb, Hq, Hkv, out=att)
+                Wo, so = self._ws(ly["o"])
+                hi.gemm(att, Wo, out=x, epi=1, scales=so)
+                self._mlp_gemm(ly, x, xn, act, eps)
+        Wl, sl = self._ws(w["lm"])
+        hi.gemv(x[n - 1:n], Wl, out=self.logits[slot:slot + 1], normw=w["nf"], eps=eps, scales=sl)
+        hi.argmax(self.logits[slot:slot + 1], out=self.tok[slot:slot + 1])
+        self.pos[slot:slot + 1].fill_(p0 + T)
+        return int(self.tok[slot].item())

@@ -88,9 +88,12 @@ def _w8(W, scales):
     return True
 
 
-def rmsnorm(x, w, eps=1e-5):
-    _dev(x, w)
-    y = torch.empty_like(x)
+def rmsnorm(x, w, eps=1e-5, out=None):
+    """y = w * fp16(x * rsqrt(mean(x^2) + eps)) per row of x [M, H] (contiguous rows)."""
+    y = torch.empty_like(x) if out is None else out
+    _dev(x, w, y)
+    if not (x.is_contiguous() and y.is_contiguous()):
+        raise ValueError("hipinfer_amd: rmsnorm rows must be contiguous")
     _ok(lib.hi_rmsnorm(_p(x), _p(w), _p(y), x.shape[0], x.shape[1], eps, _s()), "rmsnorm")
     return y
 
