@@ -197,12 +197,7 @@ def decode_step_bench(torch, hi, model, steps, ctxs=(1024, 4096)):
     max_seq = max(ctxs) + 2 * steps + 16
     res = {"config": "Llama-3.1-8B greedy decode step, batch 1, KV cache of ctx positions (synthetic), hipGraph replay"}
     for q8 in ([False, True] if model.q8 is not None else [False]):
-        layers = []
-        for l in range(L):
-            ly = {k: (model.layers[l][k] if not q8 else model.q8[l][k]) for k in SHAPES}
-            ly.update(n1=model.layers[l]["n1"], n2=model.layers[l]["n2"], bqkv=None)
-            layers.append(ly)
-        W = {"embed": embed, "lm": model.lm if not q8 else model.lm_q, "nf": model.nf, "layers": layers}
+        W = engine_weights(model, embed, q8)
         ds = DecodeStep(cfg, W, 1, max_seq)
         for k in ds.kc + ds.vc:
             k.normal_(0.0, 1.0, generator=g)
@@ -238,6 +233,75 @@ def decode_step_bench(torch, hi, model, steps, ctxs=(1024, 4096)):
                 del ga
         del gr, ds
         torch.cuda.empty_cache()
+    del embed
+    torch.cuda.empty_cache()
+    return res
+
+
+def engine_weights(model, embed, q8):
+    """The bench model's layer weights in the engine's layout (fp16, or (int8, scales))."""
+    layers = []
+    for l in range(L):
+        ly = {k: (model.layers[l][k] if not q8 else model.q8[l][k]) for k in SHAPES}
+        ly.update(n1=model.layers[l]["n1"], n2=model.layers[l]["n2"], bqkv=None)
+        layers.append(ly)
+    return {"embed": embed, "lm": model.lm if not q8 else model.lm_q, "nf": model.nf, "layers": layers}
+
+
+def engine_bench(torch, hi, model, steps, T=1024, batches=(16, 32, 64), ctx=1024):
+    """Llama-3.1-8B through the engine (hipinfer_amd.engine.DecodeStep): the prefill of a T-token
+    prompt into one cache slot (embed, 32 x [RMSNorm, QKV GEMM, RoPE/cache, flash prefill, o +
+    residual, gate/up + SwiGLU, down + residual GEMMs], final-norm lm_head GEMV, greedy; the
+    reference's prefill, api.cu:1807-1845), timed end to end on the host clock (it ends in a
+    device->host read of the token); and the greedy decode step of B sequences on the GEMM path
+    (api.cu:1914-1940) at a context of ctx positions, captured once and replayed."""
+    from hipinfer_amd.engine import DecodeStep
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEED + 21)
+    embed = torch.empty(V, H, dtype=torch.float16, device="cuda").normal_(0.0, 1.0, generator=g)
+    cfg = dict(H=H, Hq=HQ, Hkv=HKV, D=D, I=I, V=V, L=L, eps=1e-5, theta=500000.0)
+    toks = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(SEED + 22)).tolist()
+    mm_params = L * sum(N * K for N, K in SHAPES.values())
+    attn_flops = L * HQ * D * 4.0 * T * (T + 1) / 2  # QK^T and PV over the causal triangle
+    res = {"config": f"Llama-3.1-8B engine: prefill of a {T}-token prompt (one slot, one chunk); greedy decode "
+                     f"step of B sequences on the GEMM path at ctx {ctx} (synthetic caches, hipGraph replay)"}
+    for q8 in ([False, True] if model.q8 is not None else [False]):
+        tag = "int8" if q8 else "fp16"
+        W = engine_weights(model, embed, q8)
+        ds = DecodeStep(cfg, W, 1, T + 16, max_prefill=T)
+        ds.prefill(0, toks)  # first call: tunes the GEMM tiles of the M = T shapes
+        times = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            ds.prefill(0, toks)
+            times.append((time.perf_counter() - t0) * 1e3)
+        ms = sorted(times)[1]
+        flops = 2.0 * T * mm_params + attn_flops + 2.0 * V * H
+        res[f"prefill_T{T}_{tag}"] = {"ms": round(ms, 3), "tokens_per_s": round(T / ms * 1e3, 1),
+                                     "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+                                     "pct_mfma_peak": round(100 * flops / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 1)}
+        del ds
+        torch.cuda.empty_cache()
+        for B in batches:
+            ds = DecodeStep(cfg, W, B, ctx + 2 * steps + 16)
+            for k in ds.kc + ds.vc:
+                k.normal_(0.0, 1.0, generator=g)
+            ds.pos.fill_(ctx - 1)
+            ds.step()  # eager: tunes the GEMM tiles of this batch size
+            torch.cuda.synchronize()
+            gr = ds.capture()
+            ds.pos.fill_(ctx - 1)
+            ms, _ = time_graph(torch, gr, steps, 2)
+            assert torch.isfinite(ds.logits).all(), "non-finite logits (batched decode)"
+            wb = weight_bytes(q8)
+            kv = B * L * HKV * (ctx + steps) * D * 2 * 2
+            res[f"decode_B{B}_{tag}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(B / ms * 1e3, 1),
+                                        "weight_GB/s": round(wb / (ms * 1e-3) / 1e9, 1),
+                                        "GB/s": round((wb + kv) / (ms * 1e-3) / 1e9, 1),
+                                        "pct_hbm_peak": round(100 * (wb + kv) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+            del gr, ds
+            torch.cuda.empty_cache()
     del embed
     torch.cuda.empty_cache()
     return res
@@ -487,6 +551,7 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM (C3) section")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C4 / C5 sections")
     ap.add_argument("--no-step", action="store_true", help="skip the whole decode step (with attention) section")
+    ap.add_argument("--no-engine", action="store_true", help="skip the engine prefill / batched decode section")
     ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe"] +
                     [k + q for k in ("qkv", "o", "gate_up", "down", "lm_head") for q in ("", "8")], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
@@ -591,6 +656,9 @@ def main():
     if not args.no_step:
         log("decode step ...")
         res["decode_step"] = decode_step_bench(torch, hi, model, args.steps)
+    if not args.no_engine:
+        log("engine prefill / batched decode ...")
+        res["engine"] = engine_bench(torch, hi, model, args.steps)
     if not args.no_gemm:
         log("prefill GEMM ...")
         res["prefill_gemm"] = prefill_bench(torch, hi, args.steps, args.warmup, not args.no_int8)
