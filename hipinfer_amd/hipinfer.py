@@ -49,14 +49,33 @@ _OPTIONAL = {
     "hi_rope_cache": [P, I, I, I, I, I, P, P, I, I, P, P, I, P],
     "hi_flash_prefill": [P, I, P, P, I, P, I, I, I, I, I, I, P],
     "hi_flash_prefill_lse": [P, I, P, P, I, P, I, I, I, I, I, I, P, P],
+    # engine (one GPU)
+    "hi_load": [C.c_char_p, I, I, I],
+    "hi_load_tp": [C.c_char_p, I, I, I, I, P],
+    "hi_free": [P],
+    "hi_config": [P, P],
+    "hi_moe_config": [P, P],
+    "hi_weight_bytes": [P],
+    "hi_weight_quant": [P],
+    "hi_prefill": [P, I, P, I, I],
+    "hi_prefill_logits": [P, I, P, I, I, P],
+    "hi_decode": [P, I, I, I],
+    "hi_history": [P, I, I, I, P],
+    "hi_logits": [P, I, P],
+    "hi_set_state": [P, I, P, P],
+    "hi_rewind": [P, I, I, I],
+    "hi_sync": [P],
+    "hi_stream": [P],
 }
 for _name, _args in list(_SIGS.items()) + [(n, a) for n, a in _OPTIONAL.items() if hasattr(lib, n)]:
     _fn = getattr(lib, _name)
     _fn.argtypes = _args
     _fn.restype = I
-for _name in ("hi_moe_work_bytes", "hi_decode_work_bytes"):
+for _name, _rt in [("hi_moe_work_bytes", C.c_size_t), ("hi_decode_work_bytes", C.c_size_t),
+                   ("hi_weight_bytes", C.c_size_t), ("hi_load", P), ("hi_load_tp", P), ("hi_decode", F),
+                   ("hi_stream", P), ("hi_free", None), ("hi_config", None), ("hi_moe_config", None), ("hi_sync", None)]:
     if hasattr(lib, _name):
-        getattr(lib, _name).restype = C.c_size_t
+        getattr(lib, _name).restype = _rt
 MOE_NORM_TOPK, MOE_FP16_WEIGHTS = 1, 2  # moe_flags bits (reference scripts/hipinfer.py:67)
 
 
@@ -273,3 +292,91 @@ def interleave_gate_up(gate, up, group=16):
     g = gate.reshape(inter // group, group, hidden)
     u = up.reshape(inter // group, group, hidden)
     return torch.stack([g, u], dim=1).reshape(2 * inter, hidden)
+
+
+class Engine:
+    """The reference's Engine (scripts/hipinfer.py:334-500) over this library's engine entry
+    points, one GPU: a weight file in the export format (versions 2, 3, 4) loaded for max_batch
+    slots of max_seq positions, greedy prefill / decode, per-slot token history. tp must be 1.
+    Bad arguments raise ValueError (the reason is printed on stderr)."""
+
+    def __init__(self, path, max_batch=8, max_seq=2048, max_prefill=1024, tp=1, devices=None):
+        if tp != 1:
+            raise ValueError("hipinfer_amd.Engine: one GPU per engine (tp=1)")
+        dev = torch.cuda.current_device() if devices is None else list(devices)[0]
+        self.tp = 1
+        self.device = torch.device("cuda", dev)
+        self.h = lib.hi_load_tp(os.fsencode(path), max_batch, max_seq, max_prefill, 1, (C.c_int * 1)(dev))
+        if not self.h:
+            raise RuntimeError("hi_load failed")
+        cfg = (C.c_int * 11)()
+        lib.hi_config(self.h, cfg)
+        (self.vocab, self.hidden, self.inter, self.layers, self.heads, self.kv_heads, self.head_dim, self.max_pos,
+         tied, qkv_bias, self.window) = list(cfg)
+        self.tied, self.qkv_bias = bool(tied), bool(qkv_bias)
+        moe = (C.c_int * 3)()
+        lib.hi_moe_config(self.h, moe)
+        self.n_experts, self.top_k, self.moe_flags = list(moe)
+        self.quant = lib.hi_weight_quant(self.h)
+        self.max_seq, self.max_batch, self.max_prefill = max_seq, max_batch, max_prefill
+        self.weight_bytes = lib.hi_weight_bytes(self.h)
+        self.kv_bytes_per_token = 2 * self.layers * self.kv_heads * self.head_dim * 2
+
+    @staticmethod
+    def _ok(r, what):
+        if r < 0:
+            raise ValueError(f"hipinfer_amd {what}: bad arguments (see stderr)")
+        return r
+
+    def prefill(self, slot, tokens, p0=0):
+        arr = (C.c_int * len(tokens))(*tokens)
+        return self._ok(lib.hi_prefill(self.h, slot, arr, len(tokens), p0), "prefill")
+
+    def prefill_logits(self, slot, tokens, p0=0):
+        """Prefill and return the fp16 logits of every position, [T, vocab] on the GPU."""
+        arr = (C.c_int * len(tokens))(*tokens)
+        out = torch.empty(len(tokens), self.vocab, dtype=torch.float16, device=self.device)
+        self._ok(lib.hi_prefill_logits(self.h, slot, arr, len(tokens), p0, C.c_void_p(out.data_ptr())),
+                 "prefill_logits")
+        return out
+
+    def decode(self, B, steps, graph=True):
+        return self._ok(lib.hi_decode(self.h, B, steps, int(graph)), "decode")
+
+    def history(self, slot, start, n):
+        arr = (C.c_int * n)()
+        self._ok(lib.hi_history(self.h, slot, start, n, arr), "history")
+        return list(arr)
+
+    def logits(self, B):
+        out = torch.empty(B, self.vocab, dtype=torch.float16, device=self.device)
+        self._ok(lib.hi_logits(self.h, B, C.c_void_p(out.data_ptr())), "logits")
+        return out
+
+    def set_state(self, tokens, positions):
+        """Next input token and its position for slots [0, len(tokens))."""
+        B = len(tokens)
+        assert len(positions) == B
+        self._ok(lib.hi_set_state(self.h, B, (C.c_int * B)(*tokens), (C.c_int * B)(*positions)), "set_state")
+
+    def rewind(self, slot, length, next_token):
+        """Cut slot's cache to `length` positions; the next decode step feeds next_token there."""
+        self._ok(lib.hi_rewind(self.h, slot, length, next_token), "rewind")
+
+    def generate(self, prompt, n_new, graph=True):
+        """Greedy: returns n_new tokens (the first comes from prefill)."""
+        first = self.prefill(0, prompt)
+        if n_new > 1:
+            self.decode(1, n_new - 1, graph)
+        return [first] + self.history(0, len(prompt) + 1, n_new - 1)
+
+    def close(self):
+        if self.h:
+            lib.hi_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -134,6 +134,50 @@ int hi_dequantize_rows(const void* q, const void* s, long long N, int K, void* o
 /* Compute units of the current device (diagnostics; the launchers size their grids from it). */
 int hi_device_cus(void);
 
+/* ---- engine: weight-file loader, prefill, graph-captured greedy decode (one GPU)
+ * An opaque engine over a weight file in the reference's export format (scripts/export.py:5-38;
+ * versions 2 dense fp16, 3 MoE, 4 int8 projections). Per slot it keeps the next input token, its
+ * position and the token history on the device. */
+typedef struct Engine Engine;
+/* Load `path` onto the current GPU for max_batch slots of max_seq positions and prefill chunks of
+ * max_prefill rows; null (reason on stderr) for a bad file or setting. Replaces api.cu:1499. */
+Engine* hi_load(const char* path, int max_batch, int max_seq, int max_prefill);
+/* The same with a device list; world must be 1 (no tensor parallelism in this build).
+ * Replaces api.cu:1475-1497 (hi_load_tp). */
+Engine* hi_load_tp(const char* path, int max_batch, int max_seq, int max_prefill, int world, const int* devs);
+/* Replaces api.cu:1501-1507. */
+void hi_free(Engine* e);
+/* out[11]: vocab, hidden, inter, layers, heads, kv_heads, head_dim, max_pos, tied, qkv_bias,
+ * sliding window. Replaces api.cu:1509-1515. */
+void hi_config(Engine* e, int* out);
+/* out[3]: experts, top_k, MoE flags (zeros when dense). Replaces api.cu:1517-1523. */
+void hi_moe_config(Engine* e, int* out);
+/* Replaces api.cu:1525-1538. */
+size_t hi_weight_bytes(Engine* e);
+/* 0 fp16 projections, 1 int8 with fp16 row scales. Replaces api.cu:1540. */
+int hi_weight_quant(Engine* e);
+/* Prefill T host tokens into `slot` at positions p0..; returns the greedy next token (left in the
+ * slot's state, and in its history at p0 + T), or -1. Replaces api.cu:1841-1846. */
+int hi_prefill(Engine* e, int slot, const int* tokens, int T, int p0);
+/* The same, and every position's fp16 logits into dst (device, [T, vocab]). Replaces
+ * api.cu:1848-1855. */
+int hi_prefill_logits(Engine* e, int slot, const int* tokens, int T, int p0, void* dst);
+/* `steps` greedy decode steps on slots [0, B), one captured hipGraph per B when use_graph;
+ * returns GPU milliseconds, or -1. Replaces api.cu:1996-2003. */
+float hi_decode(Engine* e, int B, int steps, int use_graph);
+/* History tokens of `slot` at positions [from, from + n) to host. Replaces api.cu:2127-2142. */
+int hi_history(Engine* e, int slot, int from, int n, int* out);
+/* Latest logits of slots [0, B), fp16 [B, vocab], to host or device. Replaces api.cu:2145-2161. */
+int hi_logits(Engine* e, int B, void* dst);
+/* Next input token and position of slots [0, B). Replaces api.cu:2163-2176. */
+int hi_set_state(Engine* e, int B, const int* tok, const int* pos);
+/* Keep positions [0, len) of `slot`; the next step feeds tok at len. Replaces api.cu:2110-2123. */
+int hi_rewind(Engine* e, int slot, int len, int tok);
+/* Replaces api.cu:2125. */
+void hi_sync(Engine* e);
+/* The engine's hipStream_t. Replaces api.cu:2178. */
+void* hi_stream(Engine* e);
+
 #ifdef __cplusplus
 }
 #endif
