@@ -23,6 +23,7 @@
 #include <type_traits>
 
 #include "hi_common.h"
+#include "hi_internal.h"
 
 #ifndef HI_DA_WAVES
 #define HI_DA_WAVES 4
@@ -314,11 +315,12 @@ int decode_splits(int B, int Hkv, int cus) {
 
 template <int D>
 int decode_attn_d(int G, dim3 grid, hipStream_t s, const f16* q, int ldq, const f16* kc, const f16* vc, int max_seq,
-                  int Hkv, const int* pos, float* part, int* counters, int S, f16* out, int ldo, float sl2) {
+                  int Hkv, const int* pos, float* part, int* counters, int S, f16* out, int ldo, float sl2,
+                  int kv_slot) {
 #define HI_DA(g)                                                                                                      \
   case g:                                                                                                             \
     hipLaunchKernelGGL((decode_attn_kernel<g, D, kDaWaves>), grid, dim3(kDaWaves * 64), 0, s, q, ldq, kc, vc, max_seq, \
-                       Hkv, pos, part, counters, S, out, ldo, sl2, -1);                                               \
+                       Hkv, pos, part, counters, S, out, ldo, sl2, kv_slot);                                          \
     break;
   switch (G) {
     HI_DA(1) HI_DA(2) HI_DA(3) HI_DA(4) HI_DA(5) HI_DA(6) HI_DA(7) HI_DA(8)
@@ -400,24 +402,23 @@ HI_EXPORT size_t hi_decode_work_bytes(int B, int Hq, int Hkv, int D) {
   return (size_t)kDecodeCounters * 4 + (size_t)(B > 0 ? B : 0) * (Hq > 0 ? Hq : 0) * kDecodeMaxSplits * (D + 2) * 4;
 }
 
-// out[b, h*D : (h+1)*D] = softmax(q_h . K[0..pos[b]] / sqrt(D)) V for every query head h of
-// sequence b, K/V read from cache slot b ([slots][Hkv][max_seq][D] fp16), the kv head of h being
-// h / (Hq / Hkv). work: hi_decode_work_bytes(B, Hq, Hkv, D) bytes, zeroed once by the caller.
-HI_EXPORT int hi_decode_attn(const void* q, int ldq, const void* kc, const void* vc, int max_seq, const int* pos,
-                             void* out, int ldo, int B, int Hq, int Hkv, int D, void* work, void* s) {
+static int decode_attn_run(const void* q, int ldq, const void* kc, const void* vc, int max_seq, const int* pos,
+                           void* out, int ldo, int B, int Hq, int Hkv, int D, void* work, int kv_slot, void* s,
+                           const char* who) {
   const HiDevice* d = hi_device();
   if (!d) return -2;
-  if (D != 64 && D != 128) HI_FAIL("hi_decode_attn: head dim %d (64 or 128)", D);
+  if (D != 64 && D != 128) HI_FAIL("%s: head dim %d (64 or 128)", who, D);
   if (B < 0 || Hkv < 1 || Hq < Hkv || Hq % Hkv || Hq / Hkv > 8 || max_seq < 1)
-    HI_FAIL("hi_decode_attn: B %d, Hq %d, Hkv %d (Hq / Hkv in 1..8), max_seq %d", B, Hq, Hkv, max_seq);
+    HI_FAIL("%s: B %d, Hq %d, Hkv %d (Hq / Hkv in 1..8), max_seq %d", who, B, Hq, Hkv, max_seq);
   if (B == 0) return 0;
-  if (B * Hkv > kDecodeCounters) HI_FAIL("hi_decode_attn: B*Hkv %d > %d", B * Hkv, kDecodeCounters);
-  if (!q || !kc || !vc || !pos || !out || !work) HI_FAIL("hi_decode_attn: null pointer");
+  if (B * Hkv > kDecodeCounters) HI_FAIL("%s: B*Hkv %d > %d", who, B * Hkv, kDecodeCounters);
+  if (!q || !kc || !vc || !pos || !out || !work) HI_FAIL("%s: null pointer", who);
   if (((uintptr_t)q & 15) || ldq % 8 || ((uintptr_t)kc & 15) || ((uintptr_t)vc & 15) || ((uintptr_t)work & 3) ||
       (((uintptr_t)out) & 1))
-    HI_FAIL("hi_decode_attn: q, kc and vc must be 16-byte aligned and ldq a multiple of 8");
-  if (ldq < Hq * D || ldo < Hq * D) HI_FAIL("hi_decode_attn: ldq %d / ldo %d < Hq * D = %d", ldq, ldo, Hq * D);
-  const int S = decode_splits(B, Hkv, d->cus);
+    HI_FAIL("%s: q, kc and vc must be 16-byte aligned and ldq a multiple of 8", who);
+  if (ldq < Hq * D || ldo < Hq * D) HI_FAIL("%s: ldq %d / ldo %d < Hq * D = %d", who, ldq, ldo, Hq * D);
+  // one sequence (kv_slot >= 0): a batch of one's split count, so every row matches that decode
+  const int S = decode_splits(kv_slot >= 0 ? 1 : B, Hkv, d->cus);
   const float sl2 = 1.4426950408889634f / sqrtf((float)D);
   const dim3 grid(S, Hkv, B);
   int* counters = (int*)work;
@@ -425,9 +426,23 @@ HI_EXPORT int hi_decode_attn(const void* q, int ldq, const void* kc, const void*
   const hipStream_t st = (hipStream_t)s;
   if (D == 64)
     return decode_attn_d<64>(Hq / Hkv, grid, st, (const f16*)q, ldq, (const f16*)kc, (const f16*)vc, max_seq, Hkv, pos,
-                             part, counters, S, (f16*)out, ldo, sl2);
+                             part, counters, S, (f16*)out, ldo, sl2, kv_slot);
   return decode_attn_d<128>(Hq / Hkv, grid, st, (const f16*)q, ldq, (const f16*)kc, (const f16*)vc, max_seq, Hkv, pos,
-                            part, counters, S, (f16*)out, ldo, sl2);
+                            part, counters, S, (f16*)out, ldo, sl2, kv_slot);
+}
+
+// out[b, h*D : (h+1)*D] = softmax(q_h . K[0..pos[b]] / sqrt(D)) V for every query head h of
+// sequence b, K/V read from cache slot b ([slots][Hkv][max_seq][D] fp16), the kv head of h being
+// h / (Hq / Hkv). work: hi_decode_work_bytes(B, Hq, Hkv, D) bytes, zeroed once by the caller.
+HI_EXPORT int hi_decode_attn(const void* q, int ldq, const void* kc, const void* vc, int max_seq, const int* pos,
+                             void* out, int ldo, int B, int Hq, int Hkv, int D, void* work, void* s) {
+  return decode_attn_run(q, ldq, kc, vc, max_seq, pos, out, ldo, B, Hq, Hkv, D, work, -1, s, "hi_decode_attn");
+}
+
+int decode_attn_slot(const void* q, int ldq, const void* kc, const void* vc, int max_seq, const int* pos, void* out,
+                     int ldo, int R, int Hq, int Hkv, int D, void* work, int kv_slot, hipStream_t s) {
+  if (kv_slot < 0) HI_FAIL("decode_attn_slot: kv_slot %d < 0", kv_slot);
+  return decode_attn_run(q, ldq, kc, vc, max_seq, pos, out, ldo, R, Hq, Hkv, D, work, kv_slot, s, "decode_attn_slot");
 }
 
 // tok_out[b] = argmax of logits[b, 0:V] (fp16): NaN ranks above every number, ties go to the

@@ -3,7 +3,8 @@
 // api.cu:1807-1855), graph-captured greedy decode (hi_decode, api.cu:1891-2003), and the state
 // accessors the reference's Python Engine uses (hi_config, hi_moe_config, hi_weight_bytes,
 // hi_weight_quant, hi_history, hi_logits, hi_set_state, hi_rewind, hi_sync, hi_stream, hi_free;
-// api.cu:1501-1546, 2110-2178). One GPU: hi_load_tp accepts world = 1 only.
+// api.cu:1501-1546, 2110-2178), and speculative verification (hi_verify, hi_verify_max_rows;
+// api.cu:2018-2108). One GPU: hi_load_tp accepts world = 1 only.
 //
 // Design for MI355X:
 //  * the weight file (scripts/export.py format, versions 2 / 3 / 4) puts every tensor on a 256-byte
@@ -27,10 +28,12 @@
 
 #include "../../include/hipinfer.h"
 #include "hi_common.h"
+#include "hi_internal.h"
 
 namespace {
 
 constexpr int32_t kMagic = 0x48495046;
+constexpr int kVerifyMaxRows = 8;  // rows per verify: the GEMV path's fused-norm limit
 
 struct Cfg {
   int vocab = 0, hidden = 0, inter = 0, layers = 0, heads = 0, kv = 0, head_dim = 0, max_pos = 0, window = 0;
@@ -71,6 +74,10 @@ struct Engine {
   f16x2* rope = nullptr;
   hipStream_t st = nullptr;
   std::vector<hipGraphExec_t> graphs;
+  std::map<std::pair<int, int>, hipGraphExec_t> vgraphs;  // verify step per (slot, rows)
+  int *v_tok = nullptr, *v_pos = nullptr, *v_out = nullptr;
+  f16* v_logits = nullptr;
+  void* v_work = nullptr;
   std::vector<void*> allocs;
 };
 
@@ -125,6 +132,8 @@ void free_engine(Engine* e) {
   if (e->st) (void)hipStreamSynchronize(e->st);
   for (auto g : e->graphs)
     if (g) (void)hipGraphExecDestroy(g);
+  for (auto& g : e->vgraphs)
+    if (g.second) (void)hipGraphExecDestroy(g.second);
   for (void* p : e->allocs) (void)hipFree(p);
   if (e->st) (void)hipStreamDestroy(e->st);
   delete e;
@@ -321,10 +330,39 @@ int decode_step(Engine* e, int B) {
   return 0;
 }
 
-int capture_step(Engine* e, int B, hipGraphExec_t* out) {
+// Speculative verification rows (api.cu:2018-2067): R tokens of slot `slot` at positions v_pos
+// through the kernels of a batch-of-one decode step, R activation rows: the GEMVs (row r's
+// arithmetic does not depend on the row count) and decode attention with every query reading this
+// slot, at a batch of one's split count. All rows' k / v are written before any attention runs and
+// row r reads positions <= v_pos[r] only, so row r's logits, and the k / v it leaves, are
+// bit-identical to a plain decode step at v_pos[r]. v_out[r] = the greedy token after row r.
+int verify_step(Engine* e, int slot, int R) {
+  const Cfg& c = e->c;
+  const int H = c.hidden, D = c.head_dim, Hq = c.heads, Hkv = c.kv, HD = Hq * D, I = c.inter, V = c.vocab;
+  hipStream_t s = e->st;
+  EN_TRY(hi_embed(e->v_tok, e->embed, V, H, e->x, H, R, s));
+  for (int l = 0; l < c.layers; l++) {
+    const Layer& w = e->L[l];
+    f16* kc = e->kc + e->layer_cache * l;
+    f16* vc = e->vc + e->layer_cache * l;
+    EN_TRY(gemv_qkv_rope_slot(e->x, H, w.n1, c.eps, w.qkv.w, w.qkv.s, w.bqkv, e->qkv, e->qkv_dim, R, H, Hq, Hkv, D,
+                              e->rope, e->v_pos, kc, vc, e->max_seq, slot, s));
+    EN_TRY(decode_attn_slot(e->qkv, e->qkv_dim, kc, vc, e->max_seq, e->v_pos, e->att, HD, R, Hq, Hkv, D, e->v_work, slot,
+                            s));
+    EN_TRY(gemv(e, e->att, HD, nullptr, w.o, e->x, H, R, H, HD, 1));
+    EN_TRY(gemv(e, e->x, H, w.n2, w.gu, e->act, I, R, 2 * I, H, 2));
+    EN_TRY(gemv(e, e->act, I, nullptr, w.down, e->x, H, R, H, I, 1));
+  }
+  EN_TRY(gemv(e, e->x, H, e->final_norm, e->lm, e->v_logits, V, R, V, H, 0));
+  EN_TRY(hi_argmax(e->v_logits, R, V, e->v_out, s));
+  return 0;
+}
+
+template <class F>
+int capture(Engine* e, F step, hipGraphExec_t* out) {
   hipGraph_t g = nullptr;
   EN_TRY(hipStreamBeginCapture(e->st, hipStreamCaptureModeThreadLocal));
-  const int rc = decode_step(e, B);
+  const int rc = step();
   const hipError_t end = hipStreamEndCapture(e->st, &g);
   if (rc || end != hipSuccess) {
     if (g) (void)hipGraphDestroy(g);
@@ -333,6 +371,10 @@ int capture_step(Engine* e, int B, hipGraphExec_t* out) {
   const hipError_t ins = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
   (void)hipGraphDestroy(g);
   return ins == hipSuccess ? 0 : -2;
+}
+
+int capture_step(Engine* e, int B, hipGraphExec_t* out) {
+  return capture(e, [&] { return decode_step(e, B); }, out);
 }
 
 bool tokens_ok(const Engine* e, const int* tok, int n, const char* who) {
@@ -677,3 +719,58 @@ HI_EXPORT void hi_sync(Engine* e) {
 
 // The engine's stream (hipStream_t). Replaces api.cu:2178 (hi_stream).
 HI_EXPORT void* hi_stream(Engine* e) { return e ? (void*)e->st : nullptr; }
+
+// Rows per hi_verify call (k + 1 for k draft tokens). Replaces api.cu:2070.
+HI_EXPORT int hi_verify_max_rows() { return kVerifyMaxRows; }
+
+// Speculative verification (verify_step): the greedy next token after each of the R host tokens
+// fed at positions p0 .. p0 + R - 1 of `slot` (whose cache holds the positions below p0), into
+// out[0, R) (host); with logits_dst (device, [R, vocab] fp16) non-null the rows' logits too. The
+// rows' k / v are written to the cache; the slot's next token, position and history are left alone
+// (hi_rewind sets them). Dense models. Returns 0, or -1 for bad arguments. Replaces
+// api.cu:2077-2108 (hi_verify).
+HI_EXPORT int hi_verify(Engine* e, int slot, const int* tokens, int R, int p0, int* out, void* logits_dst,
+                        int use_graph) {
+  if (!e || e->c.moe) {
+    fprintf(stderr, "hi_verify: dense models only\n");
+    return -1;
+  }
+  if (R < 1 || R > kVerifyMaxRows || !out) {
+    fprintf(stderr, "hi_verify: R %d outside [1, %d] or null output\n", R, kVerifyMaxRows);
+    return -1;
+  }
+  if (!prefill_ok(e, slot, tokens, R, p0, "hi_verify") || hipSetDevice(e->dev) != hipSuccess) return -1;
+  hipStream_t s = e->st;
+  if (!e->v_tok) {
+    const size_t wb = hi_decode_work_bytes(kVerifyMaxRows, e->c.heads, e->c.kv, e->c.head_dim);
+    if (!(e->v_tok = (int*)dalloc(e, kVerifyMaxRows * 4)) || !(e->v_pos = (int*)dalloc(e, kVerifyMaxRows * 4)) ||
+        !(e->v_out = (int*)dalloc(e, kVerifyMaxRows * 4)) ||
+        !(e->v_logits = (f16*)dalloc(e, (size_t)kVerifyMaxRows * e->c.vocab * 2)) || !(e->v_work = dalloc(e, wb)) ||
+        hipMemsetAsync(e->v_work, 0, wb, s) != hipSuccess) {
+      e->v_tok = nullptr;
+      return -1;
+    }
+  }
+  int pos[kVerifyMaxRows];
+  for (int i = 0; i < R; i++) pos[i] = p0 + i;
+  if (hipMemcpyAsync(e->v_tok, tokens, (size_t)R * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipMemcpyAsync(e->v_pos, pos, (size_t)R * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+    return -1;
+  hipGraphExec_t& g = e->vgraphs[{slot, R}];
+  if (use_graph && g) {
+    if (hipGraphLaunch(g, s) != hipSuccess) return -1;
+  } else {
+    // eagerly (the first call of a (slot, rows) pair sets kernel attributes outside capture);
+    // the graph is captured after it for the next call
+    if (verify_step(e, slot, R)) return -1;
+    if (use_graph && (hipStreamSynchronize(s) != hipSuccess || capture(e, [&] { return verify_step(e, slot, R); }, &g)))
+      return -1;
+  }
+  if (logits_dst &&
+      hipMemcpyAsync(logits_dst, e->v_logits, (size_t)R * e->c.vocab * 2, hipMemcpyDeviceToDevice, s) != hipSuccess)
+    return -1;
+  if (hipMemcpyAsync(out, e->v_out, (size_t)R * 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return -1;
+  return 0;
+}

@@ -6,6 +6,7 @@
 // 8 (fused RMSNorm) or 16 rows, fewer when the activation rows would not fit in LDS; rows are
 // independent, so chunking never changes a result.
 #include "gemv.h"
+#include "hi_internal.h"
 
 template <> int gemv_run<0>(const GemvArgs&, int, bool, int, hipStream_t);
 template <> int gemv_run<1>(const GemvArgs&, int, bool, int, hipStream_t);
@@ -139,4 +140,13 @@ HI_EXPORT int hi_gemv_qkv_rope_w8(const void* x, int ldx, const void* normw, flo
   if (!scales) HI_FAIL("hi_gemv_qkv_rope_w8: scales must not be null");
   return qkv_common(x, ldx, normw, eps, W, scales, bias, out, ldo, M, K, Hq, Hkv, D, cs, pos, kc, vc, max_seq, -1, s,
                     "hi_gemv_qkv_rope_w8");
+}
+
+// The verify form: every row's k / v to cache slot kv_slot.
+int gemv_qkv_rope_slot(const void* x, int ldx, const void* normw, float eps, const void* W, const void* scales,
+                       const void* bias, void* out, int ldo, int M, int K, int Hq, int Hkv, int D, const void* cs,
+                       const int* pos, void* kc, void* vc, int max_seq, int kv_slot, hipStream_t s) {
+  if (kv_slot < 0) HI_FAIL("gemv_qkv_rope_slot: kv_slot %d < 0", kv_slot);
+  return qkv_common(x, ldx, normw, eps, W, scales, bias, out, ldo, M, K, Hq, Hkv, D, cs, pos, kc, vc, max_seq, kv_slot,
+                    s, "gemv_qkv_rope_slot");
 }

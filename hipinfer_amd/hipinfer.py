@@ -66,6 +66,8 @@ _OPTIONAL = {
     "hi_rewind": [P, I, I, I],
     "hi_sync": [P],
     "hi_stream": [P],
+    "hi_verify_max_rows": [],
+    "hi_verify": [P, I, P, I, I, P, P, I],
 }
 for _name, _args in list(_SIGS.items()) + [(n, a) for n, a in _OPTIONAL.items() if hasattr(lib, n)]:
     _fn = getattr(lib, _name)
@@ -362,6 +364,21 @@ class Engine:
     def rewind(self, slot, length, next_token):
         """Cut slot's cache to `length` positions; the next decode step feeds next_token there."""
         self._ok(lib.hi_rewind(self.h, slot, length, next_token), "rewind")
+
+    MAX_VERIFY = lib.hi_verify_max_rows() if hasattr(lib, "hi_verify_max_rows") else 0
+
+    def verify(self, slot, tokens, p0, graph=True, logits=False):
+        """Greedy next token after each of `tokens`, fed at positions p0.. of `slot` (whose cache
+        must hold positions < p0), computed by the batch-of-one decode kernels, so entry i is
+        exactly the token plain greedy decoding produces at p0 + i given the same prefix. Writes
+        the rows' k/v; leaves the slot's next token and position alone (see rewind). With
+        logits=True also returns the [len(tokens), vocab] fp16 logits. Dense models."""
+        R = len(tokens)
+        out = (C.c_int * R)()
+        lg = torch.empty(R, self.vocab, dtype=torch.float16, device=self.device) if logits else None
+        self._ok(lib.hi_verify(self.h, slot, (C.c_int * R)(*tokens), R, p0, out,
+                               None if lg is None else C.c_void_p(lg.data_ptr()), int(graph)), "verify")
+        return (list(out), lg) if logits else list(out)
 
     def generate(self, prompt, n_new, graph=True):
         """Greedy: returns n_new tokens (the first comes from prefill)."""

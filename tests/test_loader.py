@@ -224,3 +224,45 @@ def test_generate_graph_and_eager_agree(hi, O, tmp_path):
     finally:
         a.close()
         b.close()
+
+
+@pytest.mark.parametrize("kind", ["dense_bias", "int8"])
+def test_verify_is_bit_identical_to_greedy_decode(hi, O, tmp_path, kind):
+    """hi_verify (the reference's speculative verification, api.cu:2018-2108): R draft tokens in one
+    pass give, row for row, the logits and greedy token that plain batch-of-one decode steps give
+    when fed the same tokens at the same positions -- bit for bit -- eagerly and as a graph replay;
+    the slot's state is left alone, and hi_rewind then continues decoding from an accepted prefix."""
+    from hipinfer_amd.weights import write_weights
+    r = rng(1700 + (kind == "int8"))
+    cfg, W, _ = make_model(O, r, kind)
+    path = os.path.join(tmp_path, f"{kind}.bin")
+    write_weights(path, cfg, W)
+    prompt = r.integers(0, C["V"], 23).tolist()
+    a = hi.Engine(path, max_batch=2, max_seq=80, max_prefill=32)
+    b = hi.Engine(path, max_batch=2, max_seq=80, max_prefill=32)
+    try:
+        assert a.MAX_VERIFY == 8
+        p0 = len(prompt)
+        first = a.prefill(0, prompt)
+        assert b.prefill(0, prompt) == first
+        for R, graph in [(1, False), (5, False), (8, True), (8, True), (3, True)]:
+            draft = [first] + r.integers(0, C["V"], R - 1).tolist()
+            toks, lg = a.verify(0, draft, p0, graph=graph, logits=True)
+            lg = host(lg)
+            for i in range(R):
+                b.rewind(0, p0 + i, draft[i])
+                b.decode(1, 1)
+                ref = host(b.logits(1))[0]
+                assert np.array_equal(lg[i].view(np.uint16), ref.view(np.uint16)), (kind, R, graph, i)
+                assert toks[i] == b.history(0, p0 + i + 1, 1)[0], (kind, R, graph, i)
+        # the slot's own state was left alone: decoding from it continues from the prefill's token
+        a.rewind(0, p0, first)
+        b.rewind(0, p0, first)
+        a.decode(1, 4)
+        b.decode(1, 4, graph=False)
+        assert a.history(0, p0 + 1, 4) == b.history(0, p0 + 1, 4)
+        with pytest.raises(ValueError):
+            a.verify(0, [1] * 9, p0)  # more rows than hi_verify_max_rows
+    finally:
+        a.close()
+        b.close()
