@@ -7,12 +7,15 @@
 //  * the block stages the M activation rows in LDS once, RMSNorm'd on the way when normw is
 //    given (fused prologue, HF rounding order);
 //  * each wave owns one output unit at a time (one weight row, or the row pair an epilogue
-//    combines) and streams it with 128-bit nontemporal loads (the weights are read once), lane l
-//    taking 16-byte chunks l, l+64, ...; the first unit's loads are issued before the activation
-//    prologue and every next unit's before the current unit's reduction, so the prologue and the
-//    reductions hide under weight traffic; a unit's epilogue inputs (row scales, residual, bias,
-//    RoPE table entry) are read right after its first weights, so the epilogue waits for no
-//    dependent memory round trip;
+//    combines) and streams it with 128-bit nontemporal buffer loads (the weights are read once),
+//    lane l taking 16-byte chunks l, l+64, ...; the unit is cut into steps, and two register sets
+//    alternate so that the next step (of this unit or the wave's next one) is always in flight
+//    while the current one is computed: the first step goes out before the activation prologue,
+//    and the wave's memory pipe never idles behind its own compute, reductions or epilogues;
+//  * a step's epilogue inputs (row scales, residual, bias, RoPE table entry) travel with its
+//    weights, and every memory instruction runs on every path (buffer bounds turn the tails and
+//    the step past a wave's last unit into zero reads, dropped stores replace skipped ones), so
+//    the compiler's waits stay exact: each stage waits only for the step it computes;
 //  * int8 chunks are unpacked to exact fp16 in registers (v_perm_b32 + one packed fp16 sub per
 //    two weights) and every pair of weights meets its activation pair in one v_dot2_f32_f16
 //    (fp32 accumulate);
@@ -52,6 +55,14 @@ template <> struct WLoad<WF_I8H> { typedef u32x2 T; };
 
 constexpr int kGemvThreads = 512;              // 8 waves per block
 constexpr int kGemvWaves = kGemvThreads / kWave;
+constexpr int kRawBuffer = 0x00020000;         // buffer resource word 3: raw (untyped) 32-bit access
+constexpr int kNT = 2;                         // cache policy: nontemporal
+
+template <int WF>
+__device__ __forceinline__ typename WLoad<WF>::T load_w(__amdgpu_buffer_rsrc_t r, int off) {
+  if constexpr (WF == WF_I8H) return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kNT);
+  else return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNT);
+}
 
 template <int MR, bool NORM, int EPI, int WF, int G>
 __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
@@ -60,18 +71,27 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   constexpr int WPL = WF == WF_I8 ? 16 : 8;             // weights per load
   constexpr int XPL = WPL / 8;                          // 16-byte activation chunks per load
   constexpr int WB = WF == WF_F16 ? 16 : WPL;           // bytes per load
-  constexpr int U = R >= 8 ? 1 : 8 / R;                 // loads per row per step (8 per lane in flight)
+  // loads per row per step; two steps are in flight at any time. A step is 64 bytes of the item per
+  // lane (32 for 8-byte loads), 128 for the SwiGLU launches: measured on MI355X, launches whose
+  // waves stream several items (gate/up) run fastest on the larger steps, launches of about one
+  // item per wave (QKV, o, down) on the smaller ones, which overlap more of the item's latency.
+  constexpr int UN = (EPI == 2 ? 8 : 4) * (WF == WF_I8H ? 2 : 1);
+  constexpr int U = UN / R > 0 ? UN / R : 1;
+  constexpr int SW = 64 * U;                            // chunks of a row per step
   constexpr int XC = MR <= 8 ? (MR <= 4 ? 4 / MR : 1) : 0;  // activation chunks per row held in registers
   typedef typename WLoad<WF>::T LT;
+  typedef __amdgpu_buffer_rsrc_t RS;
   extern __shared__ u32x4 xs[];                         // [MR][K / 8] activation chunks
   __shared__ float red[kGemvWaves][MR];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = a.K, K8 = K >> 3, M = a.M;
   const int n_units = EPI >= 2 ? a.N / 2 : a.N;
   const int n_items = (n_units + G - 1) / G;
   const int nload = K / WPL;
-  const int64_t row_bytes = (int64_t)K * (WF == WF_F16 ? 2 : 1);
+  const int SPI = (nload + SW - 1) / SW;                // steps per item
+  const int row_bytes = K * (WF == WF_F16 ? 2 : 1);
   const char* Wb = reinterpret_cast<const char*>(a.W);
   const int nw = gridDim.x * kGemvWaves;
 
@@ -93,47 +113,51 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
       }
     }
   };
-  // One step of an item: U 16-byte (or 8-byte) chunks of each of its rows, streamed past the
-  // caches (nontemporal: the weights are read exactly once).
-  auto load_step = [&](LT (&wv)[R][U], const int (&rows)[R], int base) {
-#pragma unroll
-    for (int i = 0; i < U; i++) {
-      const int c = base + i * 64 + lane;
-#pragma unroll
-      for (int j = 0; j < R; j++) {
-        if (c < nload)
-          wv[j][i] = __builtin_nontemporal_load(reinterpret_cast<const LT*>(Wb + rows[j] * row_bytes + (int64_t)c * WB));
-        else
-          wv[j][i] = LT{};
-      }
-    }
-  };
 
-  // Epilogue inputs of an item's units (row scales, residual, bias, RoPE table entry), read right
-  // after the item's first weights so that none of them is a dependent memory round trip at the
-  // end of the item; kept as the raw loaded values. Lane m < M reads those of activation row m.
+  // Epilogue inputs of an item's units (row scales, residual, bias, RoPE table entry), requested
+  // with the item's weights so that none of them is a dependent memory round trip at the end of
+  // the item. Every lane loads (lanes >= M those of row M-1): the same memory instructions run on
+  // every path, which keeps the compiler's waits for each step's weights exact.
   struct Pre {
     f16 s0, s1, r, b0, b1;
     f16x2 cs;
   };
-  const bool epi_lane = lane < MR && lane < M;
-  const int my_pos = (EPI == 3 && epi_lane) ? a.pos[lane] : 0;
-  auto load_pre = [&](Pre (&pre)[G], int t, const int (&rows)[R]) {
-    if (!epi_lane) return;
+  const int lm = min(lane, M - 1);
+  const int my_pos = EPI == 3 ? a.pos[lm] : 0;
+  // bias reads through a buffer of 0 bytes when there is no bias: zeros, no memory access
+  const RS bias_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(a.bias), (short)0,
+                                                       (EPI == 3 && a.bias) ? a.N * 2 : 0, kRawBuffer);
+
+  // One step of item t (step s: chunks s*SW .. s*SW+SW-1 of each row) and its epilogue inputs.
+  // Chunks past the row's end, and every chunk of an item past the last, read as zeros through
+  // the buffer bounds without a memory access.
+  auto issue = [&](LT (&wv)[R][U], Pre (&pre)[G], int t, int s) {
+    int rows[R];
+    item_rows(t, rows);
+    const int nbytes = t < n_items ? row_bytes : 0;
+    RS rs[R];
+#pragma unroll
+    for (int j = 0; j < R; j++)
+      rs[j] = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(Wb + (int64_t)rows[j] * row_bytes), (short)0, nbytes,
+                                                kRawBuffer);
+#pragma unroll
+    for (int i = 0; i < U; i++) {
+      const int off = (s * SW + i * 64 + lane) * WB;
+#pragma unroll
+      for (int j = 0; j < R; j++) wv[j][i] = load_w<WF>(rs[j], off);
+    }
 #pragma unroll
     for (int g = 0; g < G; g++) {
       const int u = min(t * G + g, n_units - 1);
       if constexpr (WF != WF_F16) {
         pre[g].s0 = a.scales[rows[g * NR]];
-        pre[g].s1 = a.scales[rows[g * NR + NR - 1]];
+        pre[g].s1 = NR == 2 ? a.scales[rows[g * NR + NR - 1]] : pre[g].s0;
       }
-      if constexpr (EPI == 1) pre[g].r = a.out[lane * a.ldo + u];
+      if constexpr (EPI == 1) pre[g].r = a.out[lm * a.ldo + u];
       if constexpr (EPI == 3) {
         const int HD = a.D >> 1;
-        if (a.bias) {
-          pre[g].b0 = a.bias[rows[g * NR]];
-          pre[g].b1 = a.bias[rows[g * NR + NR - 1]];
-        }
+        pre[g].b0 = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(bias_rs, rows[g * NR] * 2, 0, 0));
+        pre[g].b1 = __builtin_bit_cast(f16, __builtin_amdgcn_raw_buffer_load_b16(bias_rs, rows[g * NR + NR - 1] * 2, 0, 0));
         pre[g].cs = a.cs[(int64_t)my_pos * HD + u % HD];
       }
     }
@@ -155,16 +179,10 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
     }
   }
   // ---- 2. the first step of this wave's first item
-  LT wv[R][U];
-  int rows[R];
-  Pre pn[G] = {};  // the epilogue inputs of the item whose first step is in flight
-  const int t0 = blockIdx.x * kGemvWaves + wave;
-  bool have = t0 < n_items;
-  if (have) {
-    item_rows(t0, rows);
-    load_step(wv, rows, 0);
-    load_pre(pn, t0, rows);
-  }
+  LT wa[R][U], wb[R][U];
+  Pre pa[G] = {}, pb[G] = {};
+  int t = blockIdx.x * kGemvWaves + wave, s = 0;  // the step in flight in (wa, pa)
+  issue(wa, pa, t, 0);
   // ---- 3. stage the activation rows in LDS, RMSNorm'd (HF order) when normw is given; rows >= M
   //         are zero so no garbage reaches the sums
   if constexpr (NORM) {
@@ -260,105 +278,167 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   }
   __syncthreads();
 
-  // ---- 4. stream the items; each item's next-item prefetch is issued before its reduction.
-  //         Every activation chunk read from LDS feeds all R rows of the item, and each row's
-  //         products are summed in the same order for every G, so G never changes a result.
-  for (int t = t0; t < n_items; t += nw) {
-    Pre pc[G];
+  // ---- 4. stream the steps: each stage requests the next step (into the other register set)
+  //         before computing its own, so a wave always has a step of weights in flight. Every
+  //         activation chunk read from LDS feeds all R rows of the item, and each row's products
+  //         are summed in the same order for every G and step size, so neither changes a result.
+  float acc[R][MR];
 #pragma unroll
-    for (int g = 0; g < G; g++) pc[g] = pn[g];
-    float acc[R][MR];
+  for (int j = 0; j < R; j++)
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[j][m] = 0.f;
+  const bool epi_lane = lane < MR && lane < M;
+  const int n_out = EPI == 2 ? a.N / 2 : a.N;
+  // epilogues 0-2 store through a buffer: lanes without a row write at its end, where the store
+  // is dropped, so every lane runs the same store instructions
+  const uint32_t out_bytes = (uint32_t)(((int64_t)(M - 1) * a.ldo + n_out) * 2);
+  const RS out_rs = __builtin_amdgcn_make_buffer_rsrc(a.out, (short)0, (int)out_bytes, kRawBuffer);
+
+  auto stage = [&](LT (&cur)[R][U], Pre (&pc)[G], LT (&nxt)[R][U], Pre (&pn)[G]) {
+    t = __builtin_amdgcn_readfirstlane(t);  // wave-uniform: keeps every buffer resource in SGPRs
+    s = __builtin_amdgcn_readfirstlane(s);
+    int tn = t, sn = s + 1;
+    if (sn == SPI) {
+      sn = 0;
+      tn += nw;
+    }
+    issue(nxt, pn, tn, sn);
+    // this step's weights and epilogue inputs: consumed here, on every path (the compute below
+    // skips lanes past the row's end), so no load into a register is still pending when the loop
+    // comes round and the compiler's waits at the loop head stay exact
 #pragma unroll
     for (int j = 0; j < R; j++)
 #pragma unroll
-      for (int m = 0; m < MR; m++) acc[j][m] = 0.f;
-
-    for (int base = 0; base < nload; base += 64 * U) {
-      if (!have) load_step(wv, rows, base);
-      have = false;
+      for (int i = 0; i < U; i++) asm volatile("" ::"v"(cur[j][i]));
 #pragma unroll
-      for (int i = 0; i < U; i++) {
-        const int c = base + i * 64 + lane;
-        if (c < nload) {
+    for (int g = 0; g < G; g++) {
+      if constexpr (WF != WF_F16) asm volatile("" ::"v"(pc[g].s0), "v"(pc[g].s1));
+      if constexpr (EPI == 1) asm volatile("" ::"v"(pc[g].r));
+      if constexpr (EPI == 3) asm volatile("" ::"v"(pc[g].b0), "v"(pc[g].b1), "v"(pc[g].cs));
+    }
+    const int base = s * SW;
 #pragma unroll
-          for (int q = 0; q < XPL; q++) {
-            u32x4 xv[MR];
+    for (int i = 0; i < U; i++) {
+      const int c = base + i * 64 + lane;
+      if (c < nload) {
 #pragma unroll
-            for (int m = 0; m < MR; m++) xv[m] = xs[m * K8 + c * XPL + q];
+        for (int q = 0; q < XPL; q++) {
+          u32x4 xv[MR];
 #pragma unroll
-            for (int j = 0; j < R; j++) {
-              f16x2 w4[4];  // the 8 weights of this row that meet activation chunk q
-              if constexpr (WF == WF_F16) {
+          for (int m = 0; m < MR; m++) xv[m] = xs[m * K8 + c * XPL + q];
 #pragma unroll
-                for (int p = 0; p < 4; p++) w4[p] = as_h2(wv[j][i][p]);
-              } else {
-                i8x4_to_f16(wv[j][i][2 * q], w4[0], w4[1]);
-                i8x4_to_f16(wv[j][i][2 * q + 1], w4[2], w4[3]);
-              }
+          for (int j = 0; j < R; j++) {
+            f16x2 w4[4];  // the 8 weights of this row that meet activation chunk q
+            if constexpr (WF == WF_F16) {
 #pragma unroll
-              for (int m = 0; m < MR; m++)
-#pragma unroll
-                for (int p = 0; p < 4; p++) acc[j][m] = dot2(w4[p], as_h2(xv[m][p]), acc[j][m]);
+              for (int p = 0; p < 4; p++) w4[p] = as_h2(cur[j][i][p]);
+            } else {
+              i8x4_to_f16(cur[j][i][2 * q], w4[0], w4[1]);
+              i8x4_to_f16(cur[j][i][2 * q + 1], w4[2], w4[3]);
             }
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+#pragma unroll
+              for (int p = 0; p < 4; p++) acc[j][m] = dot2(w4[p], as_h2(xv[m][p]), acc[j][m]);
           }
         }
       }
     }
-
-    if (t + nw < n_items) {
-      item_rows(t + nw, rows);
-      load_step(wv, rows, 0);
-      load_pre(pn, t + nw, rows);
-      have = true;
-    }
-
+    // epilogues 0-2 store on every stage (a dropped store except on an item's last step), so the
+    // stages issue the same memory instructions whichever way the branch below goes
+    f16 y[G], y2[G];
 #pragma unroll
-    for (int j = 0; j < R; j++)
+    for (int g = 0; g < G; g++) y[g] = y2[g] = (f16)0.f;
+    const bool last = s == SPI - 1;
+    if (last) {
 #pragma unroll
-      for (int m = 0; m < MR; m++) acc[j][m] = wave_sum(acc[j][m]);
-
-    if (epi_lane) {
+      for (int j = 0; j < R; j++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[j][m] = wave_sum(acc[j][m]);
 #pragma unroll
       for (int g = 0; g < G; g++) {
         const int u = t * G + g;
-        if (u >= n_units) break;
         float a0 = 0.f, a1 = 0.f;  // this lane's row, selected without dynamic register indexing
 #pragma unroll
         for (int m = 0; m < MR; m++)
-          if (m == lane) {
+          if (m == lm) {
             a0 = acc[g * NR][m];
             a1 = acc[g * NR + NR - 1][m];
           }
         if constexpr (WF != WF_F16) {
           a0 *= (float)pc[g].s0;  // the row scale applied once to the reduced sum (reference kernels.cuh:261)
           a1 *= (float)pc[g].s1;
+          // the fp32 product is rounded before its conversion to fp16 (two roundings, as the
+          // reference's fp32 multiply then __float2half): no fused mixed-precision fma
+          asm volatile("" : "+v"(a0), "+v"(a1));
         }
-        f16* orow = a.out + lane * a.ldo;
         if constexpr (EPI == 0) {
-          orow[u] = (f16)a0;
+          y[g] = (f16)a0;
         } else if constexpr (EPI == 1) {
-          orow[u] = pc[g].r + (f16)a0;  // fp16 add, correctly rounded
+          y[g] = pc[g].r + (f16)a0;  // fp16 add, correctly rounded
         } else if constexpr (EPI == 2) {
-          orow[u] = silu_mul(a0, a1);
+          y[g] = silu_mul(a0, a1);
         } else {
-          const int D = a.D, HD = D >> 1, head = u / HD, d = u - head * HD;
-          const int p = my_pos;
-          const int slot = a.kv_slot >= 0 ? a.kv_slot : a.slot_base + lane;
           if (a.bias) {
             a0 += (float)pc[g].b0;
             a1 += (float)pc[g].b1;
+            asm volatile("" : "+v"(a0), "+v"(a1));  // fp32 sum, then fp16: two roundings
           }
-          f16 y1 = (f16)a0, y2 = (f16)a1;
-          if (head < a.Hq + a.Hkv) rope_pair(y1, y2, pc[g].cs);
-          f16* dst;
-          if (head < a.Hq) dst = orow + head * D;
-          else if (head < a.Hq + a.Hkv) dst = a.kc + (((int64_t)slot * a.Hkv + head - a.Hq) * a.max_seq + p) * D;
-          else dst = a.vc + (((int64_t)slot * a.Hkv + head - a.Hq - a.Hkv) * a.max_seq + p) * D;
-          dst[d] = y1;
-          dst[d + HD] = y2;
+          f16 r1 = (f16)a0, r2 = (f16)a1;
+          const int HD = a.D >> 1;
+          if (min(u, n_units - 1) / HD < a.Hq + a.Hkv) rope_pair(r1, r2, pc[g].cs);
+          y[g] = r1;
+          y2[g] = r2;
         }
       }
+#pragma unroll
+      for (int j = 0; j < R; j++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[j][m] = 0.f;
     }
+    if constexpr (EPI <= 2) {
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        const int u = t * G + g;
+        const uint32_t off = (last && epi_lane && u < n_units) ? (uint32_t)((lane * a.ldo + u) * 2) : out_bytes;
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, y[g]), out_rs, (int)off, 0, 0);
+      }
+    } else {
+      // q to out[row, head*D + d], k / v to the cache at (slot, kv head, pos, d), through a buffer
+      // whose base is uniform (out, or this launch's first slot's kv head in the cache) and which
+      // holds no records except on an item's last step. Lanes past the last row repeat that row's
+      // stores (same values, same addresses). The host keeps every offset below 4 GB.
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        const int u = min(t * G + g, n_units - 1);
+        const int D = a.D, HD = D >> 1, head = u / HD, d = u - head * HD;
+        const f16* base;
+        uint32_t off;
+        if (head < a.Hq) {
+          base = a.out;
+          off = (uint32_t)(lm * a.ldo + head * D + d);
+        } else {
+          const bool isk = head < a.Hq + a.Hkv;
+          const int kvh = head - a.Hq - (isk ? 0 : a.Hkv);
+          const int sb = a.kv_slot >= 0 ? a.kv_slot : a.slot_base, dl = a.kv_slot >= 0 ? 0 : lm;
+          base = (isk ? a.kc : a.vc) + ((int64_t)sb * a.Hkv + kvh) * a.max_seq * D;
+          off = (uint32_t)(((int64_t)dl * a.Hkv * a.max_seq + my_pos) * D + d);
+        }
+        const uint64_t bp = reinterpret_cast<uint64_t>(base);  // wave-uniform: a resource in SGPRs
+        const uint32_t blo = __builtin_amdgcn_readfirstlane((uint32_t)bp), bhi = __builtin_amdgcn_readfirstlane((uint32_t)(bp >> 32));
+        const RS rs = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<f16*>(((uint64_t)bhi << 32) | blo), (short)0,
+                                                        __builtin_amdgcn_readfirstlane(last ? -1 : 0), kRawBuffer);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, y[g]), rs, (int)(off * 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, y2[g]), rs, (int)((off + HD) * 2), 0, 0);
+      }
+    }
+    t = tn;
+    s = sn;
+  };
+  while (t < n_items) {
+    stage(wa, pa, wb, pb);
+    if (t >= n_items) break;
+    stage(wb, pb, wa, pa);
   }
 }
 
@@ -375,15 +455,11 @@ int gemv_launch(const GemvArgs& a, hipStream_t s) {
   if (bpc == 0) HI_FAIL("gemv: %zu bytes of activation rows do not fit in LDS", lds);
   const int n_units = EPI >= 2 ? a.N / 2 : a.N;
   const int n_items = (n_units + G - 1) / G;
-  const int slots = bpc * d->cus * kGemvWaves;
-  const int per_wave = (n_items + slots - 1) / slots;
-  int grid = (n_items + kGemvWaves * per_wave - 1) / (kGemvWaves * per_wave);
-  // An equal split that would leave CUs idle (items just above the resident slots) gives way to
-  // every resident block, the waves taking items in grid stride (counts within one of each other).
-  if (grid < d->cus) {
-    const int all = (n_items + kGemvWaves - 1) / kGemvWaves;
-    grid = all < bpc * d->cus ? all : bpc * d->cus;
-  }
+  // One item per wave while the items fit the resident slots; past that, exactly the resident
+  // blocks (bpc on every CU), the waves taking items in grid stride, so every CU streams the same
+  // share of the weights (wave counts within one item of each other).
+  const int one_each = (n_items + kGemvWaves - 1) / kGemvWaves;
+  const int grid = one_each < bpc * d->cus ? one_each : bpc * d->cus;
   hipLaunchKernelGGL((gemv_kernel<MR, NORM, EPI, WF, G>), dim3(grid), dim3(kGemvThreads), lds, s, a);
   HI_TRY(hipGetLastError());
   return 0;

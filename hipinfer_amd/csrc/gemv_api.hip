@@ -35,6 +35,16 @@ static int gemv_common(GemvArgs a, int epi, hipStream_t s, const char* who) {
   const bool norm = a.normw != nullptr;
   int cap = norm ? 8 : 16;
   while (cap > 1 && (size_t)cap * a.K * 2 > (size_t)d->lds_max) cap >>= 1;
+  if (epi == 3) {
+    // the fused QKV epilogue writes a launch's cache rows at 32-bit byte offsets from its first
+    // slot (and q rows from out): fewer rows per launch when a slot is large
+    const uint64_t lim = 0xFFFFFFFFull, pos_bytes = (uint64_t)a.max_seq * a.D * 2;
+    const uint64_t slot_bytes = pos_bytes * a.Hkv;
+    if (pos_bytes > lim) HI_FAIL("%s: a cache head of %d x %d fp16 exceeds 4 GB", who, a.max_seq, a.D);
+    if (a.kv_slot < 0)
+      while (cap > 1 && (uint64_t)(cap - 1) * slot_bytes + pos_bytes > lim) cap >>= 1;
+    if (((uint64_t)(cap - 1) * a.ldo + (uint64_t)a.Hq * a.D) * 2 > lim) HI_FAIL("%s: ldo %lld too large", who, (long long)a.ldo);
+  }
   const int M = a.M;
   for (int m0 = 0; m0 < M; m0 += cap) {
     GemvArgs c = a;

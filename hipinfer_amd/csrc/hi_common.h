@@ -113,7 +113,9 @@ __device__ __forceinline__ f16 silu_mul(float g, float u) {
 // boundary (then it is one fp16 ulp off). For epilogues that produce thousands of values per lane.
 __device__ __forceinline__ f16 silu_mul_fast(float g, float u) {
   const float gh = (float)(f16)g;
-  const f16 s = (f16)(gh * __builtin_amdgcn_rcpf(1.0f + __expf(-gh)));
+  float q = gh * __builtin_amdgcn_rcpf(1.0f + __expf(-gh));
+  asm volatile("" : "+v"(q));  // fp32 product, then fp16: not one fused mixed-precision rounding
+  const f16 s = (f16)q;
   return s * (f16)u;
 }
 

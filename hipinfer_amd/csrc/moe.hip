@@ -219,13 +219,18 @@ __global__ void __launch_bounds__(kMoeWaves * 64) moe_gemv_down_kernel(const f16
 #pragma unroll
   for (int j = 0; j < KM; j++) {
     if (j < k && ex[j] >= 0 && ex[j] < E) {  // uniform over the wave
-      const float c = (float)(f16)wave_sum(acc[j]) * wts[(int64_t)b * k + j];
+      float c = (float)(f16)wave_sum(acc[j]) * wts[(int64_t)b * k + j];
+      asm volatile("" : "+v"(c));  // the fp32 product is what gets rounded to fp16
       sum += (flags & kMoeFp16Weights) ? (float)(f16)c : c;
     }
   }
   if (lane == 0) {
     f16 o = (f16)sum;
-    if (scale != 1.f) o = (f16)((float)o * scale);
+    if (scale != 1.f) {
+      float t = (float)o * scale;
+      asm volatile("" : "+v"(t));  // fp32 product, then fp16 (two roundings)
+      o = (f16)t;
+    }
     f16* dst = x + (int64_t)b * ldx + h;
     *dst = *dst + o;
   }
@@ -300,7 +305,8 @@ __global__ void __launch_bounds__(128) moe_combine_kernel(const f16* __restrict_
       const f16x8 v = *reinterpret_cast<const f16x8*>(y + (int64_t)q * H + 8 * i);
 #pragma unroll
       for (int u = 0; u < 8; u++) {
-        const float c = (float)v[u] * w;
+        float c = (float)v[u] * w;
+        asm volatile("" : "+v"(c));  // the fp32 product is what gets rounded to fp16
         s[u] += (flags & kMoeFp16Weights) ? (float)(f16)c : c;
       }
     }
@@ -308,7 +314,11 @@ __global__ void __launch_bounds__(128) moe_combine_kernel(const f16* __restrict_
 #pragma unroll
     for (int u = 0; u < 8; u++) {
       f16 o = (f16)s[u];
-      if (scale != 1.f) o = (f16)((float)o * scale);
+      if (scale != 1.f) {
+        float t = (float)o * scale;
+        asm volatile("" : "+v"(t));  // fp32 product, then fp16 (two roundings)
+        o = (f16)t;
+      }
       xv[u] = xv[u] + o;
     }
     *reinterpret_cast<f16x8*>(xr + 8 * i) = xv;
