@@ -486,7 +486,8 @@ def decode_config_bench(torch, hi, name, dims, M_list, n_layers, steps, seed, q8
 def moe_bench(torch, hi, steps, seed):
     """Granite-3.1-1B-A400M-shaped MoE layers (hidden 1024, 32 experts of SwiGLU 1024 -> 2 x 512 and
     512 -> 1024, top-8, softmax over the top-8 logits, fp16 routing weights, residual scale 0.22) over
-    24 distinct layers: B = 1 decode (router + GEMV experts) and a 256-token prefill (router +
+    24 distinct layers: B = 1 decode as the reference's two calls (router, then GEMV experts) and as
+    this library's one call (router inside the gate/up launch), and a 256-token prefill (router +
     grouped MFMA experts)."""
     H, E, I, k, L = 1024, 32, 512, 8, 24
     flags = hi.MOE_NORM_TOPK | hi.MOE_FP16_WEIGHTS
@@ -496,7 +497,7 @@ def moe_bench(torch, hi, steps, seed):
     wdn = [torch.empty(E, H, I, dtype=torch.float16, device="cuda").normal_(0, 0.02, generator=g) for _ in range(L)]
     res = {"config": "Granite-3.1-1B-A400M MoE layer: H 1024, 32 experts (gate/up 1024->2x512, down 512->1024), "
                      "top-8, 24 distinct layers per step"}
-    for M, path, tag in [(1, 1, "decode_B1_gemv"), (256, 2, "prefill_256_grouped")]:
+    for M, path, tag in [(1, 1, "decode_B1_gemv"), (1, -1, "decode_B1_fused"), (256, 2, "prefill_256_grouped")]:
         xn = torch.randn(M, H, generator=g, device="cuda").half()
         x0 = torch.randn(M, H, generator=g, device="cuda").half()
         x = x0.clone()
@@ -507,6 +508,11 @@ def moe_bench(torch, hi, steps, seed):
         def step():
             x.copy_(x0)
             for l in range(L):
+                if path < 0:  # router + experts in one call
+                    hi.lib.hi_moe_route_experts(hi._p(xn), xn.stride(0), hi._p(Wr[l]), hi._p(wgu[l]), hi._p(wdn[l]), M,
+                                                E, k, H, I, flags, 0.22, hi._p(x), x.stride(0), hi._p(idx),
+                                                hi._p(wts), hi._p(work), hi._s())
+                    continue
                 hi.lib.hi_moe_router(hi._p(xn), xn.stride(0), hi._p(Wr[l]), M, E, H, k, flags, hi._p(idx), hi._p(wts),
                                      hi._s())
                 hi.lib.hi_moe_experts(hi._p(xn), xn.stride(0), hi._p(wgu[l]), hi._p(wdn[l]), hi._p(idx), hi._p(wts), M,

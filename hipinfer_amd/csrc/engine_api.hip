@@ -272,9 +272,10 @@ int moe_rows(Engine* e, const Layer& w, f16* x, f16* xn, int m) {
   const Cfg& c = e->c;
   const int H = c.hidden;
   EN_TRY(hi_rmsnorm(x, w.n2, xn, m, H, c.eps, e->st));
-  EN_TRY(hi_moe_router(xn, H, w.router, m, c.n_experts, H, c.top_k, c.moe_flags, e->moe_idx, e->moe_w, e->st));
-  EN_TRY(hi_moe_experts(xn, H, w.ewgu, w.ewdown, e->moe_idx, e->moe_w, m, c.n_experts, c.top_k, H, c.inter,
-                        c.moe_flags, c.moe_scale, x, H, 0, e->moe_work, e->st));
+  // router and experts in one call: the same bits as the reference's two calls, with the router
+  // inside the gate/up launch on the GEMV path
+  EN_TRY(hi_moe_route_experts(xn, H, w.router, w.ewgu, w.ewdown, m, c.n_experts, c.top_k, H, c.inter, c.moe_flags,
+                              c.moe_scale, x, H, e->moe_idx, e->moe_w, e->moe_work, e->st));
   return 0;
 }
 

@@ -41,25 +41,23 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float best, int bi
 }
 
 // ------------------------------------------------------------------ router
-// One block of 16 waves per token row; each wave computes two experts' logits with all the row's
-// loads issued together (CH chunks of 8 halves per lane per round), so a row costs about one memory
-// round trip. The top k are then chosen by rank: argmax_better is a strict total order on (logit,
-// index), so the expert that exactly j others beat is the j-th pick of the sequential argmax, and
-// every expert's rank is counted in parallel from the logits in LDS.
+// The router's three steps, shared by the router kernel and the fused decode kernel so that both
+// produce the same bits:
+//  * logits: the block's waves take experts two at a time, each loading the row's chunks and both
+//    expert rows together (CH chunks of 8 halves per lane per round), so a row costs about one
+//    memory round trip; every expert's dot product runs in the same order whatever the number of
+//    waves; rounded to fp16 (the router linear's output dtype);
+//  * top k by rank: argmax_better is a strict total order on (logit, index), so the expert that
+//    exactly j others beat is the j-th pick of the sequential argmax, and every expert's rank is
+//    counted in parallel from the logits in LDS;
+//  * weights: softmax over the k (norm_topk) or over all E, rounded to fp16 when the model rounds.
 constexpr int kRouterWaves = 16;
 template <int CH>
-__global__ void __launch_bounds__(kRouterWaves * 64) moe_router_kernel(const f16* __restrict__ xn, int64_t ldx,
-                                                                      const f16* __restrict__ Wr, int E, int H, int k,
-                                                                      int flags, int* __restrict__ idx_out,
-                                                                      float* __restrict__ w_out) {
-  __shared__ float logit[kMoeMaxE];
-  __shared__ float selv[kMoeMaxK];
-  __shared__ int seli[kMoeMaxK];
-  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const f16* xr = xn + t * ldx;
+__device__ __forceinline__ void router_logits(const f16* __restrict__ xr, const f16* __restrict__ Wr, int E, int H,
+                                              int nwaves, int wave, int lane, float* logit) {
   const int H8 = H / 8;
-  for (int e0 = wave; e0 < E; e0 += 2 * kRouterWaves) {
-    const int e1 = e0 + kRouterWaves;
+  for (int e0 = wave; e0 < E; e0 += 2 * nwaves) {
+    const int e1 = e0 + nwaves;
     const f16* w0 = Wr + (int64_t)e0 * H;
     const f16* w1 = Wr + (int64_t)min(e1, E - 1) * H;
     float a0 = 0.f, a1 = 0.f;
@@ -91,8 +89,11 @@ __global__ void __launch_bounds__(kRouterWaves * 64) moe_router_kernel(const f16
       if (e1 < E) logit[e1] = (float)(f16)a1;
     }
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += kRouterWaves * 64) {
+}
+
+__device__ __forceinline__ void router_topk(const float* logit, int E, int k, int tid, int nthreads, float* selv,
+                                            int* seli) {
+  for (int e = tid; e < E; e += nthreads) {
     const float v = logit[e];
     int r = 0;
 #pragma unroll 8
@@ -102,8 +103,12 @@ __global__ void __launch_bounds__(kRouterWaves * 64) moe_router_kernel(const f16
       selv[r] = v;
     }
   }
-  __syncthreads();
-  if (wave != 0) return;
+}
+
+// One wave: the k weights of token t into idx_out / w_out (descending by logit).
+__device__ __forceinline__ void router_weights(const float* logit, const float* selv, const int* seli, int E, int k,
+                                               int flags, int lane, int t, int* __restrict__ idx_out,
+                                               float* __restrict__ w_out) {
   const float mx = selv[0];
   float denom = 0.f;
   if (flags & kMoeNormTopk) {
@@ -119,6 +124,23 @@ __global__ void __launch_bounds__(kRouterWaves * 64) moe_router_kernel(const f16
     idx_out[(int64_t)t * k + lane] = seli[lane];
     w_out[(int64_t)t * k + lane] = wj;
   }
+}
+
+// One block of 16 waves per token row.
+template <int CH>
+__global__ void __launch_bounds__(kRouterWaves * 64) moe_router_kernel(const f16* __restrict__ xn, int64_t ldx,
+                                                                      const f16* __restrict__ Wr, int E, int H, int k,
+                                                                      int flags, int* __restrict__ idx_out,
+                                                                      float* __restrict__ w_out) {
+  __shared__ float logit[kMoeMaxE];
+  __shared__ float selv[kMoeMaxK];
+  __shared__ int seli[kMoeMaxK];
+  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  router_logits<CH>(xn + t * ldx, Wr, E, H, kRouterWaves, wave, lane, logit);
+  __syncthreads();
+  router_topk(logit, E, k, threadIdx.x, kRouterWaves * 64, selv, seli);
+  __syncthreads();
+  if (wave == 0) router_weights(logit, selv, seli, E, k, flags, lane, t, idx_out, w_out);
 }
 
 // Chunks of 8 halves per lane per load round for a row of n halves: one round covers the row up to
@@ -167,6 +189,65 @@ __global__ void __launch_bounds__(kMoeWaves * 64) moe_gemv_gu_kernel(const f16* 
         const f16x2 x2 = as_h2(ok ? xv[j][q] : 0u);
         ag = dot2(as_h2(gv[j][q]), x2, ag);
         au = dot2(as_h2(uv[j][q]), x2, au);
+      }
+    }
+  }
+  ag = wave_sum(ag);
+  au = wave_sum(au);
+  if (lane == 0) act[(int64_t)p * I + o] = silu_mul(ag, au);
+}
+
+// Router + gate/up + SwiGLU in one launch (the GEMV path of hi_moe_route_experts): a block of 16
+// waves serves one token-slot pair p = t*k + j and 16 consecutive units (I % 16 == 0), so it first
+// computes token t's logits and top k with the router's own steps and wave count (the same bits as
+// moe_router_kernel, in one memory round trip for E <= 32; every block reads the router weights,
+// E*H*2 bytes, mostly from L2), then streams slot j's expert rows as moe_gemv_gu_kernel does. The
+// block of pair t*k and unit 0 also writes the token's idx / w, which the down projection reads.
+constexpr int kFusedWaves = kRouterWaves;
+template <int CH>
+__global__ void __launch_bounds__(kFusedWaves * 64) moe_route_gu_kernel(const f16* __restrict__ xn, int64_t ldx,
+                                                                      const f16* __restrict__ Wr,
+                                                                      const f16* __restrict__ wgu, int n, int k, int E,
+                                                                      int H, int I, int flags, int* __restrict__ idx_out,
+                                                                      float* __restrict__ w_out, f16* __restrict__ act) {
+  __shared__ float logit[kMoeMaxE];
+  __shared__ float selv[kMoeMaxK];
+  __shared__ int seli[kMoeMaxK];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t w0 = (int64_t)blockIdx.x * kFusedWaves;
+  const int p = (int)(w0 / I), t = p / k, j = p - t * k;
+  const f16* xr = xn + (int64_t)t * ldx;
+  router_logits<CH>(xr, Wr, E, H, kFusedWaves, wave, lane, logit);
+  __syncthreads();
+  router_topk(logit, E, k, threadIdx.x, kFusedWaves * 64, selv, seli);
+  __syncthreads();
+  if (j == 0 && w0 == (int64_t)p * I && wave == 0) router_weights(logit, selv, seli, E, k, flags, lane, t, idx_out, w_out);
+  const int64_t w = w0 + wave;
+  if (w >= (int64_t)n * I) return;
+  const int o = (int)(w - (int64_t)p * I);
+  const int e = seli[j];
+  const int r0 = (o >> 4) * 32 + (o & 15);
+  const f16* g = wgu + ((int64_t)e * 2 * I + r0) * H;
+  const f16* u = g + 16 * (int64_t)H;
+  const int H8 = H / 8;
+  float ag = 0.f, au = 0.f;
+  for (int b = 0; b < H8; b += 64 * CH) {
+    u32x4 xv[CH], gv[CH], uv[CH];
+#pragma unroll
+    for (int q = 0; q < CH; q++) {
+      const int c = b + q * 64 + lane, cc = c < H8 ? c : 0;
+      xv[q] = *reinterpret_cast<const u32x4*>(xr + 8 * cc);
+      gv[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g + 8 * cc));
+      uv[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(u + 8 * cc));
+    }
+#pragma unroll
+    for (int q = 0; q < CH; q++) {
+      const bool ok = b + q * 64 + lane < H8;
+#pragma unroll
+      for (int h = 0; h < 4; h++) {
+        const f16x2 x2 = as_h2(ok ? xv[q][h] : 0u);
+        ag = dot2(as_h2(gv[q][h]), x2, ag);
+        au = dot2(as_h2(uv[q][h]), x2, au);
       }
     }
   }
@@ -365,6 +446,35 @@ int gemv_max() {
   return v < 8 ? v : 8;
 }
 
+// The expert workspace (hi_moe_work_bytes), each piece on a 256-byte boundary.
+struct MoeWork {
+  int *perm, *inv, *off, *tiles;
+  f16 *rows, *y, *act;
+};
+MoeWork moe_work(void* work, int n, int E, int H) {
+  char* p = (char*)work;
+  MoeWork m;
+  m.perm = (int*)p;   p += al256((size_t)n * 4);
+  m.inv = (int*)p;    p += al256((size_t)n * 4);
+  m.off = (int*)p;    p += al256((size_t)(E + 1) * 4);
+  m.tiles = (int*)p;  p += al256((size_t)(E + 1) * 4);
+  m.rows = (f16*)p;   p += al256((size_t)n * H * 2);
+  m.y = (f16*)p;      p += al256((size_t)n * H * 2);
+  m.act = (f16*)p;
+  return m;
+}
+
+// The GEMV path's down projection + weighted combine + residual.
+int moe_down_launch(const f16* act, const f16* Wd, const int* idx, const float* w, int M, int k, int E, int H, int I,
+                    int flags, float scale, void* x, int ldx, hipStream_t st) {
+  const int64_t dn_waves = (int64_t)M * H;
+  const auto dn = k <= 4 ? moe_gemv_down_kernel<4> : k <= 8 ? moe_gemv_down_kernel<8> : moe_gemv_down_kernel<16>;
+  hipLaunchKernelGGL(dn, dim3((unsigned)((dn_waves + kMoeWaves - 1) / kMoeWaves)), dim3(kMoeWaves * 64), 0, st, act,
+                     Wd, idx, w, M, k, E, H, I, flags, scale, (f16*)x, (int64_t)ldx);
+  HI_TRY(hipGetLastError());
+  return 0;
+}
+
 }  // namespace
 
 // Router + top-k for M normalised rows xn: idx[M, k] (int) and weights w[M, k] (fp32), descending.
@@ -411,29 +521,25 @@ HI_EXPORT int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const vo
     HI_FAIL("hi_moe_experts: tensors must be 16-byte aligned (work 256-byte), ldxn and ldx multiples of 8");
   const hipStream_t st = (hipStream_t)s;
   const int n = M * k;
-  char* p = (char*)work;
-  int* perm = (int*)p;   p += al256((size_t)n * 4);
-  int* inv = (int*)p;    p += al256((size_t)n * 4);
-  int* off = (int*)p;    p += al256((size_t)(E + 1) * 4);
-  int* tiles = (int*)p;  p += al256((size_t)(E + 1) * 4);
-  f16* rows = (f16*)p;   p += al256((size_t)n * H * 2);
-  f16* y = (f16*)p;      p += al256((size_t)n * H * 2);
-  f16* act = (f16*)p;
+  const MoeWork wk = moe_work(work, n, E, H);
   const f16* Wgu = (const f16*)wgu;
   const f16* Wd = (const f16*)wdown;
   if (path == 1 || (path == 0 && M <= gemv_max())) {
-    const int64_t gu_waves = (int64_t)n * I, dn_waves = (int64_t)M * H;
+    const int64_t gu_waves = (int64_t)n * I;
     const auto gu = chunks_for(H) == 1 ? moe_gemv_gu_kernel<1> : chunks_for(H) == 2 ? moe_gemv_gu_kernel<2>
                                                                                     : moe_gemv_gu_kernel<4>;
     hipLaunchKernelGGL(gu, dim3((unsigned)((gu_waves + kMoeWaves - 1) / kMoeWaves)), dim3(kMoeWaves * 64),
-                       0, st, (const f16*)xn, (int64_t)ldxn, Wgu, idx, n, k, E, H, I, act);
+                       0, st, (const f16*)xn, (int64_t)ldxn, Wgu, idx, n, k, E, H, I, wk.act);
     HI_TRY(hipGetLastError());
-    const auto dn = k <= 4 ? moe_gemv_down_kernel<4> : k <= 8 ? moe_gemv_down_kernel<8> : moe_gemv_down_kernel<16>;
-    hipLaunchKernelGGL(dn, dim3((unsigned)((dn_waves + kMoeWaves - 1) / kMoeWaves)),
-                       dim3(kMoeWaves * 64), 0, st, act, Wd, idx, w, M, k, E, H, I, flags, scale, (f16*)x, (int64_t)ldx);
-    HI_TRY(hipGetLastError());
-    return 0;
+    return moe_down_launch(wk.act, Wd, idx, w, M, k, E, H, I, flags, scale, x, ldx, st);
   }
+  int* perm = wk.perm;
+  int* inv = wk.inv;
+  int* off = wk.off;
+  int* tiles = wk.tiles;
+  f16* rows = wk.rows;
+  f16* y = wk.y;
+  f16* act = wk.act;
   hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(1024), 0, st, idx, n, E, off, tiles, perm, inv);
   HI_TRY(hipGetLastError());
   hipLaunchKernelGGL(moe_gather_kernel, dim3(n), dim3(128), 0, st, (const f16*)xn, (int64_t)ldxn, perm, off, E, k, H, rows);
@@ -445,4 +551,40 @@ HI_EXPORT int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const vo
   hipLaunchKernelGGL(moe_combine_kernel, dim3(M), dim3(128), 0, st, y, inv, w, k, H, flags, scale, (f16*)x, (int64_t)ldx);
   HI_TRY(hipGetLastError());
   return 0;
+}
+
+// Router and experts in one call: x[m] += MoE(xn[m]) for M rows, with the routing computed here and
+// written to idx / w as hi_moe_router writes it. The same bits as hi_moe_router followed by
+// hi_moe_experts with path 0. On the GEMV path (M <= HIPINFER_GEMV_MAX) the router runs inside
+// the gate/up launch (moe_route_gu_kernel), which saves a launch and a dependent memory round trip
+// per layer; larger M run the router and the grouped experts as two calls. No counterpart in the
+// reference, whose engine makes the two calls (api.cu:1701-1703); this build's engine uses this.
+HI_EXPORT int hi_moe_route_experts(const void* xn, int ldxn, const void* Wr, const void* wgu, const void* wdown, int M,
+                                   int E, int k, int H, int I, int flags, float scale, void* x, int ldx, int* idx,
+                                   float* w, void* work, void* s) {
+  const HiDevice* d = hi_device();
+  if (!d) return -2;
+  if (M < 0) HI_FAIL("hi_moe_route_experts: M %d < 0", M);
+  if (M == 0) return 0;
+  if (M > gemv_max()) {
+    if (int r = hi_moe_router(xn, ldxn, Wr, M, E, H, k, flags, idx, w, s)) return r;
+    return hi_moe_experts(xn, ldxn, wgu, wdown, idx, w, M, E, k, H, I, flags, scale, x, ldx, 0, work, s);
+  }
+  if (E < 1 || E > kMoeMaxE || k < 1 || k > kMoeMaxK || k > E)
+    HI_FAIL("hi_moe_route_experts: unsupported E %d / k %d (E <= %d, k <= %d, k <= E)", E, k, kMoeMaxE, kMoeMaxK);
+  if (H % 32 || I % 32 || H < 32 || I < 32) HI_FAIL("hi_moe_route_experts: H %d and I %d must be multiples of 32", H, I);
+  if (!xn || !Wr || !wgu || !wdown || !idx || !w || !x || !work) HI_FAIL("hi_moe_route_experts: null pointer");
+  if (((uintptr_t)xn & 15) || ((uintptr_t)Wr & 15) || ((uintptr_t)wgu & 15) || ((uintptr_t)wdown & 15) ||
+      ((uintptr_t)x & 15) || ((uintptr_t)work & 255) || ldxn % 8 || ldx % 8)
+    HI_FAIL("hi_moe_route_experts: tensors must be 16-byte aligned (work 256-byte), ldxn and ldx multiples of 8");
+  const hipStream_t st = (hipStream_t)s;
+  const int n = M * k;
+  const MoeWork wk = moe_work(work, n, E, H);
+  const int64_t gu_waves = (int64_t)n * I;
+  const auto gu = chunks_for(H) == 1 ? moe_route_gu_kernel<1> : chunks_for(H) == 2 ? moe_route_gu_kernel<2>
+                                                                                  : moe_route_gu_kernel<4>;
+  hipLaunchKernelGGL(gu, dim3((unsigned)(gu_waves / kFusedWaves)), dim3(kFusedWaves * 64), 0, st, (const f16*)xn,
+                     (int64_t)ldxn, (const f16*)Wr, (const f16*)wgu, n, k, E, H, I, flags, idx, w, wk.act);
+  HI_TRY(hipGetLastError());
+  return moe_down_launch(wk.act, (const f16*)wdown, idx, w, M, k, E, H, I, flags, scale, x, ldx, st);
 }

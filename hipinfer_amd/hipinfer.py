@@ -42,6 +42,7 @@ _OPTIONAL = {
     "hi_moe_router": [P, I, P, I, I, I, I, I, P, P, P],
     "hi_moe_work_bytes": [I, I, I, I, I],
     "hi_moe_experts": [P, I, P, P, P, P, I, I, I, I, I, I, F, P, I, I, P, P],
+    "hi_moe_route_experts": [P, I, P, P, P, I, I, I, I, I, I, F, P, I, P, P, P, P],
     "hi_decode_work_bytes": [I, I, I, I],
     "hi_decode_attn": [P, I, P, P, I, P, P, I, I, I, I, I, P, P],
     "hi_argmax": [P, I, I, P, P],
@@ -187,6 +188,21 @@ def moe_experts(xn, wgu, wdown, idx, w, x, flags, scale=1.0, path=0):
     _ok(lib.hi_moe_experts(_p(xn), xn.stride(0), _p(wgu), _p(wdown), _p(idx), _p(w), M, E, k, H, I, flags, scale, _p(x),
                            x.stride(0), path, _p(work), _s()), "moe_experts")
     return x
+
+
+def moe_route_experts(xn, Wr, wgu, wdown, k, x, flags, scale=1.0):
+    """Router and experts in one call: x += MoE(xn) in place with the routing computed on the way;
+    returns (idx [M, k] int32, weights [M, k] fp32) as moe_router would. The same bits as moe_router
+    then moe_experts(path=0); up to HIPINFER_GEMV_MAX rows the router runs inside the gate/up launch."""
+    M, H = xn.shape
+    E, I = wgu.shape[0], wdown.shape[2]
+    _dev(xn, Wr, wgu, wdown, x)
+    idx = torch.empty(M, k, dtype=torch.int32, device=xn.device)
+    w = torch.empty(M, k, dtype=torch.float32, device=xn.device)
+    work = torch.empty(lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device=xn.device)
+    _ok(lib.hi_moe_route_experts(_p(xn), xn.stride(0), _p(Wr), _p(wgu), _p(wdown), M, E, k, H, I, flags, scale, _p(x),
+                                 x.stride(0), _p(idx), _p(w), _p(work), _s()), "moe_route_experts")
+    return idx, w
 
 
 # ------------------------------------------------------------------ int8 weight format (GPU)

@@ -81,6 +81,15 @@ size_t hi_moe_work_bytes(int M, int k, int E, int H, int I);
 int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const void* wdown, const int* idx, const float* w, int M,
                    int E, int k, int H, int I, int flags, float scale, void* x, int ldx, int path, void* work,
                    void* stream);
+/* Router and experts in one call: x[m] += MoE(xn[m]) with the routing computed here and written to
+ * idx[M, k] / w[M, k] as hi_moe_router writes it; the same bits as hi_moe_router followed by
+ * hi_moe_experts(path 0). For M <= HIPINFER_GEMV_MAX the router runs inside the gate/up launch (one
+ * launch and one dependent memory round trip fewer per layer). work: hi_moe_work_bytes(M, k, E, H, I).
+ * No counterpart in the reference (its engine makes the two calls, api.cu:1701-1703); for callers
+ * that run a whole MoE layer, such as this library's engine. */
+int hi_moe_route_experts(const void* xn, int ldxn, const void* Wr, const void* wgu, const void* wdown, int M, int E,
+                         int k, int H, int I, int flags, float scale, void* x, int ldx, int* idx, float* w, void* work,
+                         void* stream);
 
 /* ---- decode-step kernels around the GEMVs
  * Bytes of the workspace hi_decode_attn needs: 4096 int counters (zeroed once by the caller, left

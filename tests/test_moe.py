@@ -136,3 +136,68 @@ def test_moe_rejects_bad_arguments(hi):
     w = torch.ones(2, 1, dtype=torch.float32, device="cuda")
     with pytest.raises(ValueError):
         hi.moe_experts(xn, wgu, wdn, idx, w, xn.clone(), 1)  # H = 48 is not a multiple of 32
+
+
+@pytest.mark.parametrize("name,E,k,H,I,flags,scale", LAYERS, ids=[l[0] for l in LAYERS])
+def test_moe_route_experts_is_router_then_experts(hi, name, E, k, H, I, flags, scale):
+    """hi_moe_route_experts (router inside the gate/up launch up to HIPINFER_GEMV_MAX rows, the two
+    calls above it) gives the same bits as hi_moe_router followed by hi_moe_experts(path 0): the
+    routing (indices, order, weights) and the updated residual, at M on both sides of the limit."""
+    r = rng(440 + E)
+    Wr = cuda(rn(r, E, H, s=0.05))
+    wgu, wdn = cuda(rn(r, E, 2 * I, H, s=0.02)), cuda(rn(r, E, H, I, s=0.02))
+    for M in [1, 2, 3, 4, 5, 37]:
+        xn, x0 = cuda(rn(r, M, H)), cuda(rn(r, M, H))
+        idx2, w2 = hi.moe_router(xn, Wr, k, flags)
+        ref = host(hi.moe_experts(xn, wgu, wdn, idx2, w2, x0.clone(), flags, scale, 0))
+        x = x0.clone()
+        idx, w = hi.moe_route_experts(xn, Wr, wgu, wdn, k, x, flags, scale)
+        assert np.array_equal(host(idx), host(idx2)), f"{name} M={M}: routing differs"
+        assert np.array_equal(host(w).view(np.uint32), host(w2).view(np.uint32)), f"{name} M={M}: weights differ"
+        assert np.array_equal(host(x).view(np.uint16), ref.view(np.uint16)), f"{name} M={M}: output differs"
+
+
+def test_moe_route_experts_graph_replay(hi):
+    """The fused decode call captured in a graph: every replay, with eager work between, equals the
+    eager two-call result bit for bit."""
+    import torch
+    r = rng(450)
+    E, k, H, I, flags, M = 32, 8, 1024, 512, 3, 1
+    Wr, wgu, wdn = cuda(rn(r, E, H, s=0.05)), cuda(rn(r, E, 2 * I, H, s=0.02)), cuda(rn(r, E, H, I, s=0.02))
+    xn, x0 = cuda(rn(r, M, H)), cuda(rn(r, M, H))
+    idx2, w2 = hi.moe_router(xn, Wr, k, flags)
+    ref = host(hi.moe_experts(xn, wgu, wdn, idx2, w2, x0.clone(), flags, 0.22, 0))
+    x = x0.clone()
+    idx = torch.empty(M, k, dtype=torch.int32, device="cuda")
+    w = torch.empty(M, k, dtype=torch.float32, device="cuda")
+    work = torch.empty(hi.lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device="cuda")
+
+    def run():
+        hi._ok(hi.lib.hi_moe_route_experts(hi._p(xn), H, hi._p(Wr), hi._p(wgu), hi._p(wdn), M, E, k, H, I, flags, 0.22,
+                                           hi._p(x), H, hi._p(idx), hi._p(w), hi._p(work), hi._s()), "moe_route_experts")
+    run()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    for _ in range(3):
+        x.copy_(x0)
+        idx.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(x).view(np.uint16), ref.view(np.uint16))
+        assert np.array_equal(host(idx), host(idx2))
+        hi.moe_route_experts(xn, Wr, wgu, wdn, k, x0.clone(), flags, 0.22)  # eager work between replays
+
+
+def test_moe_route_experts_rejects_bad_arguments(hi):
+    import torch
+    xn = torch.zeros(1, 64, dtype=torch.float16, device="cuda")
+    Wr = torch.zeros(4, 64, dtype=torch.float16, device="cuda")
+    wgu = torch.zeros(4, 64, 64, dtype=torch.float16, device="cuda")
+    wdn = torch.zeros(4, 64, 32, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        hi.moe_route_experts(xn, Wr, wgu, wdn, 5, xn.clone(), 1)  # k > E
+    with pytest.raises(ValueError):
+        hi.moe_route_experts(xn[:, :48], Wr[:, :48], wgu[:, :, :48], wdn[:, :48], 2, xn[:, :48].clone(), 1)  # H = 48
