@@ -44,6 +44,9 @@ static int gemv_common(GemvArgs a, int epi, hipStream_t s, const char* who) {
     if (a.kv_slot < 0)
       while (cap > 1 && (uint64_t)(cap - 1) * slot_bytes + pos_bytes > lim) cap >>= 1;
     if (((uint64_t)(cap - 1) * a.ldo + (uint64_t)a.Hq * a.D) * 2 > lim) HI_FAIL("%s: ldo %lld too large", who, (long long)a.ldo);
+  } else if (((uint64_t)(cap - 1) * a.ldo + (uint64_t)n_out) * 2 > 0xFFFFFFFFull) {
+    // epilogues 0-2 store through a buffer at 32-bit byte offsets from a launch's first row
+    HI_FAIL("%s: ldo %lld too large (a launch's output rows must span under 4 GB)", who, (long long)a.ldo);
   }
   const int M = a.M;
   for (int m0 = 0; m0 < M; m0 += cap) {
