@@ -180,32 +180,69 @@ HI_EXPORT int hi_dequantize_rows(const void* q, const void* s, long long N, int 
 
 // ------------------------------------------------------------------ standalone RMSNorm
 // y = w * fp16(x * (1 / sqrt(mean x^2 + eps))), one block per row, rows contiguous.
+// One block per row. Rows of up to 8192 halves stay in registers between the sum of squares and
+// the scaling (one read of the row), and the norm weight is requested before the reduction; the
+// sums run in the same chunk order either way.
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
                                                      f16* __restrict__ y, int H, float eps) {
+  constexpr int RC = 4;  // 16-byte chunks per thread held in registers
   __shared__ float red[4];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, n8 = H / 8;
   const f16* xr = x + (int64_t)blockIdx.x * H;
   f16* yr = y + (int64_t)blockIdx.x * H;
+  const bool held = n8 <= RC * 256;
+  u32x4 xv[RC], wv[RC];
   float ss = 0.f;
-  for (int i = tid; i < H / 8; i += 256) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + 8 * i);
+  if (held) {
 #pragma unroll
-    for (int p = 0; p < 4; p++) {
-      const f16x2 h = as_h2(v[p]);
-      ss = dot2(h, h, ss);
+    for (int j = 0; j < RC; j++) {
+      const int c = tid + j * 256;
+      xv[j] = c < n8 ? *reinterpret_cast<const u32x4*>(xr + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+      wv[j] = c < n8 ? *reinterpret_cast<const u32x4*>(w + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < RC; j++)
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const f16x2 h = as_h2(xv[j][p]);
+        ss = dot2(h, h, ss);
+      }
+  } else {
+    for (int i = tid; i < n8; i += 256) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(xr + 8 * i);
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const f16x2 h = as_h2(v[p]);
+        ss = dot2(h, h, ss);
+      }
     }
   }
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   const float r = 1.0f / __builtin_sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)H + eps);
-  for (int i = tid; i < H / 8; i += 256) {
-    const f16x8 v = *reinterpret_cast<const f16x8*>(xr + 8 * i);
-    const f16x8 wv = *reinterpret_cast<const f16x8*>(w + 8 * i);
-    f16x8 o;
+  auto scale = [&](u32x4 xc, u32x4 wc) {
+    u32x4 o;
 #pragma unroll
-    for (int j = 0; j < 8; j++) o[j] = wv[j] * (f16)((float)v[j] * r);
-    *reinterpret_cast<f16x8*>(yr + 8 * i) = o;
+    for (int p = 0; p < 4; p++) {
+      const f16x2 xh = as_h2(xc[p]), wh = as_h2(wc[p]);
+      f16x2 t;
+      t.x = wh.x * (f16)((float)xh.x * r);
+      t.y = wh.y * (f16)((float)xh.y * r);
+      o[p] = as_u32(t);
+    }
+    return o;
+  };
+  if (held) {
+#pragma unroll
+    for (int j = 0; j < RC; j++) {
+      const int c = tid + j * 256;
+      if (c < n8) *reinterpret_cast<u32x4*>(yr + 8 * c) = scale(xv[j], wv[j]);
+    }
+  } else {
+    for (int i = tid; i < n8; i += 256)
+      *reinterpret_cast<u32x4*>(yr + 8 * i) =
+          scale(*reinterpret_cast<const u32x4*>(xr + 8 * i), *reinterpret_cast<const u32x4*>(w + 8 * i));
   }
 }
 

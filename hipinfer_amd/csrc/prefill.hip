@@ -208,6 +208,43 @@ __global__ void __launch_bounds__(256)
     vc[(((int64_t)slot * Hkv + i / D) * max_seq + p) * D + i % D] = v[i];
 }
 
+// The same with 16-byte accesses: a thread step rotates 8 pairs of one head (the 8 elements at d
+// and the 8 at d + D/2, and their 8 table entries) or copies 8 elements of v. Used when D/2 is a
+// multiple of 8 and every row, cache and the table are 16-byte aligned; each pair is rotated by
+// rope_pair, as above, so the two kernels give the same bits.
+__global__ void __launch_bounds__(256)
+    rope_cache_v8_kernel(f16* qkv, int64_t ldq, int Hq, int Hkv, int D, const f16x2* __restrict__ cs,
+                         const int* __restrict__ pos, int pos_base, int slot_base, f16* kc, f16* vc, int max_seq) {
+  const int HD = D / 2, C = HD / 8, row = blockIdx.x;
+  const int p = pos ? pos[row] : pos_base + row;
+  const int slot = pos ? slot_base + row : slot_base;
+  f16* base = qkv + (int64_t)row * ldq;
+  const int nrot = (Hq + Hkv) * C, nv = Hkv * D / 8;
+  for (int i = threadIdx.x; i < nrot + nv; i += blockDim.x) {
+    if (i < nrot) {
+      const int hh = i / C, d = (i - hh * C) * 8;
+      f16* x = base + hh * D;
+      f16x8 a = *reinterpret_cast<const f16x8*>(x + d), b = *reinterpret_cast<const f16x8*>(x + d + HD);
+      const u32x4* tp = reinterpret_cast<const u32x4*>(cs + (int64_t)p * HD + d);
+      const u32x4 c0 = tp[0], c1 = tp[1];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        f16 y1 = a[j], y2 = b[j];
+        rope_pair(y1, y2, as_h2(j < 4 ? c0[j] : c1[j - 4]));
+        a[j] = y1;
+        b[j] = y2;
+      }
+      f16* dst = hh < Hq ? x : kc + (((int64_t)slot * Hkv + hh - Hq) * max_seq + p) * D;
+      *reinterpret_cast<f16x8*>(dst + d) = a;
+      *reinterpret_cast<f16x8*>(dst + d + HD) = b;
+    } else {
+      const int c = i - nrot, h = c / (D / 8), e = (c - h * (D / 8)) * 8;
+      *reinterpret_cast<u32x4*>(vc + (((int64_t)slot * Hkv + h) * max_seq + p) * D + e) =
+          *reinterpret_cast<const u32x4*>(base + (Hq + Hkv + h) * D + e);
+    }
+  }
+}
+
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 int flash_prefill(const void* q, int ldq, const void* kc, const void* vc, int max_seq, void* out, int ldo, int T,
@@ -251,8 +288,9 @@ HI_EXPORT int hi_rope_cache(void* qkv, int ldq, int M, int Hq, int Hkv, int D, c
   if (!pos && (pos_base < 0 || (int64_t)pos_base + M > max_seq))
     HI_FAIL("hi_rope_cache: positions %d..%d outside the cache (max_seq %d)", pos_base, pos_base + M - 1, max_seq);
   if (!aligned(cs, 4)) HI_FAIL("hi_rope_cache: cs must be 4-byte aligned");
-  hipLaunchKernelGGL(rope_cache_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, (f16*)qkv, (int64_t)ldq, Hq, Hkv, D,
-                     (const f16x2*)cs, pos, pos_base, slot_base, (f16*)kc, (f16*)vc, max_seq);
+  const bool v8 = D % 16 == 0 && ldq % 8 == 0 && aligned(qkv, 16) && aligned(cs, 16) && aligned(kc, 16) && aligned(vc, 16);
+  hipLaunchKernelGGL(v8 ? rope_cache_v8_kernel : rope_cache_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, (f16*)qkv,
+                     (int64_t)ldq, Hq, Hkv, D, (const f16x2*)cs, pos, pos_base, slot_base, (f16*)kc, (f16*)vc, max_seq);
   HI_TRY(hipGetLastError());
   return 0;
 }
