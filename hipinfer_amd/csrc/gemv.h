@@ -16,9 +16,10 @@
 //    weights, and every memory instruction runs on every path (buffer bounds turn the tails and
 //    the step past a wave's last unit into zero reads, dropped stores replace skipped ones), so
 //    the compiler's waits stay exact: each stage waits only for the step it computes;
-//  * int8 chunks are unpacked to exact fp16 in registers (v_perm_b32 + one packed fp16 sub per
-//    two weights) and every pair of weights meets its activation pair in one v_dot2_f32_f16
-//    (fp32 accumulate);
+//  * int8 chunks are unpacked to exact fp16 1152 + q in registers (one v_perm_b32 per two
+//    weights; each lane's sums start at -1152 times the activation elements it meets, so the
+//    offset is never subtracted per weight) and every pair of weights meets its activation pair
+//    in one v_dot2_f32_f16 (fp32 accumulate);
 //  * a fixed DPP/swizzle butterfly reduces each row over the wave; the int8 row scale is applied
 //    once to the reduced sum, then the epilogue runs on lane m for activation row m.
 // A row's arithmetic never depends on M, the unit schedule or the grid: row m of an M-row GEMV is
@@ -81,8 +82,10 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   constexpr int XC = MR <= 8 ? (MR <= 4 ? 4 / MR : 1) : 0;  // activation chunks per row held in registers
   typedef typename WLoad<WF>::T LT;
   typedef __amdgpu_buffer_rsrc_t RS;
+  constexpr bool BIAS = WF != WF_F16;                    // int8 weights unpacked with an offset (below)
   extern __shared__ u32x4 xs[];                         // [MR][K / 8] activation chunks
   __shared__ float red[kGemvWaves][MR];
+  __shared__ float xp[BIAS ? MR : 1][BIAS ? kGemvThreads : 1];  // per staging thread: its chunks' sum
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -184,7 +187,19 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   int t = blockIdx.x * kGemvWaves + wave, s = 0;  // the step in flight in (wa, pa)
   issue(wa, pa, t, 0);
   // ---- 3. stage the activation rows in LDS, RMSNorm'd (HF order) when normw is given; rows >= M
-  //         are zero so no garbage reaches the sums
+  //         are zero so no garbage reaches the sums. Thread t stages chunks t, t + 512, ... of
+  //         every row, in that order on every path, and (int8) sums each row's chunks as it goes.
+  float xsum[BIAS ? MR : 1];
+#pragma unroll
+  for (int m = 0; m < (BIAS ? MR : 1); m++) xsum[m] = 0.f;
+  auto put = [&](int m, int c, u32x4 v) {
+    xs[m * K8 + c] = v;
+    if constexpr (BIAS) {
+      const f16x2 one = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+      for (int p = 0; p < 4; p++) xsum[m] = dot2(as_h2(v[p]), one, xsum[m]);
+    }
+  };
   if constexpr (NORM) {
     float ss[MR];
 #pragma unroll
@@ -245,7 +260,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
         const int c = tid + j * kGemvThreads;
         if (c < K8) {
 #pragma unroll
-          for (int m = 0; m < MR; m++) xs[m * K8 + c] = m < M ? norm_chunk(xr[m][j], nr[j], r[m]) : u32x4{0u, 0u, 0u, 0u};
+          for (int m = 0; m < MR; m++) put(m, c, m < M ? norm_chunk(xr[m][j], nr[j], r[m]) : u32x4{0u, 0u, 0u, 0u});
         }
       }
     } else {
@@ -253,8 +268,8 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
         const u32x4 wn = *reinterpret_cast<const u32x4*>(a.normw + 8 * c);
 #pragma unroll
         for (int m = 0; m < MR; m++)
-          xs[m * K8 + c] = m < M ? norm_chunk(*reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c), wn, r[m])
-                                 : u32x4{0u, 0u, 0u, 0u};
+          put(m, c, m < M ? norm_chunk(*reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c), wn, r[m])
+                          : u32x4{0u, 0u, 0u, 0u});
       }
     }
   } else {
@@ -264,17 +279,19 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
         const int c = tid + j * kGemvThreads;
         if (c < K8) {
 #pragma unroll
-          for (int m = 0; m < MR; m++) xs[m * K8 + c] = xr[m][j];
+          for (int m = 0; m < MR; m++) put(m, c, xr[m][j]);
         }
       }
     } else {
-      for (int i = tid; i < MR * K8; i += kGemvThreads) {
-        const int m = i / K8, c = i - m * K8;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (m < M) v = *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c);
-        xs[i] = v;
-      }
+      for (int c = tid; c < K8; c += kGemvThreads)
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+          put(m, c, m < M ? *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c) : u32x4{0u, 0u, 0u, 0u});
     }
+  }
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int m = 0; m < MR; m++) xp[m][tid] = xsum[m];
   }
   __syncthreads();
 
@@ -282,11 +299,32 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   //         before computing its own, so a wave always has a step of weights in flight. Every
   //         activation chunk read from LDS feeds all R rows of the item, and each row's products
   //         are summed in the same order for every G and step size, so neither changes a result.
+  // int8 rows are unpacked as 1152 + q (one packed fp16 subtraction fewer per two weights), so a
+  // lane's sums carry 1152 times the sum of the activation elements it meets (chunks c = lane mod
+  // 64 of each row, whatever the step size); they start at minus that, from the partial sums of
+  // the staging threads that hold those elements. The offset depends only on the activation row
+  // and the lane, so row independence and the one-hot exactness hold as for unbiased sums.
+  float x0[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) x0[m] = 0.f;
+  if constexpr (BIAS) {
+    // staging thread t holds activation chunks t + 512 j: those of lane (t mod 128) / 2 for
+    // 16-byte weight loads (two chunks per load), of lane t mod 64 for 8-byte ones; eight threads
+    // per lane, summed in thread order
+    static_assert(kGemvThreads == 512, "the partial-sum lanes assume 512 staging threads");
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      float v = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; i++) v += xp[m][XPL == 2 ? 2 * lane + (i & 1) + 128 * (i >> 1) : lane + 64 * i];
+      x0[m] = v * -1152.0f;
+    }
+  }
   float acc[R][MR];
 #pragma unroll
   for (int j = 0; j < R; j++)
 #pragma unroll
-    for (int m = 0; m < MR; m++) acc[j][m] = 0.f;
+    for (int m = 0; m < MR; m++) acc[j][m] = x0[m];
   const bool epi_lane = lane < MR && lane < M;
   const int n_out = EPI == 2 ? a.N / 2 : a.N;
   // epilogues 0-2 store through a buffer: lanes without a row write at its end, where the store
@@ -333,8 +371,8 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
 #pragma unroll
               for (int p = 0; p < 4; p++) w4[p] = as_h2(cur[j][i][p]);
             } else {
-              i8x4_to_f16(cur[j][i][2 * q], w4[0], w4[1]);
-              i8x4_to_f16(cur[j][i][2 * q + 1], w4[2], w4[3]);
+              i8x4_to_f16_biased(cur[j][i][2 * q], w4[0], w4[1]);
+              i8x4_to_f16_biased(cur[j][i][2 * q + 1], w4[2], w4[3]);
             }
 #pragma unroll
             for (int m = 0; m < MR; m++)
@@ -394,7 +432,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int j = 0; j < R; j++)
 #pragma unroll
-        for (int m = 0; m < MR; m++) acc[j][m] = 0.f;
+        for (int m = 0; m < MR; m++) acc[j][m] = x0[m];
     }
     if constexpr (EPI <= 2) {
 #pragma unroll

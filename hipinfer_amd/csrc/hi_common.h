@@ -95,6 +95,15 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t w, f16x2& lo, f16x2& hi) {
 
 __device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
 
+// The same four weights offset by 1152: 1152 + q exactly, without the subtraction (one v_xor and
+// two v_perm_b32 per four weights). A dot product over them carries 1152 times the sum of the
+// activations it met, which the caller removes (the GEMV starts each sum at -1152 * that sum).
+__device__ __forceinline__ void i8x4_to_f16_biased(uint32_t w, f16x2& lo, f16x2& hi) {
+  const uint32_t b = w ^ 0x80808080u;
+  lo = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u));
+  hi = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u));
+}
+
 // A 32-bit word as two fp16 values. Always go through this (a scalar parameter): this clang folds
 // __builtin_bit_cast applied directly to a vector element `v[p]` to element 0 of `v`.
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
