@@ -538,6 +538,8 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(const float* __restric
 // waves stacked along M, each 32 rows by the whole width) cut N = 5120 and N = 3072 at M = 1024
 // into exactly 256 tiles, one per CU, with no split-K. 32 x 256 (four waves side by side, 32 x 64
 // each) serves batched decode (M <= 32) on the widest projections: 32 KB of weights per stage.
+// 256 x 192 (eight waves of 64 x 96) cuts N = 3072 at M = 1024 into 64 big tiles, 256 blocks with
+// a 4-way split-K: half the staged bytes of 128 x 96 for the same K range.
 struct GemmCfg {
   int bm, bn, wm, wn, st, bk;
 };
@@ -546,7 +548,7 @@ constexpr GemmCfg kGemmCfgs[] = {{256, 256, 2, 2, 2, 64}, {256, 128, 2, 2, 3, 64
                                  {32, 128, 1, 4, 4, 64},  {128, 64, 2, 2, 4, 64},  {256, 256, 2, 4, 2, 64},
                                  {256, 128, 2, 4, 3, 64}, {256, 256, 2, 4, 4, 32}, {256, 128, 2, 2, 6, 32},
                                  {128, 256, 2, 4, 6, 32}, {128, 160, 4, 1, 4, 64}, {128, 96, 4, 1, 4, 64},
-                                 {32, 256, 1, 4, 4, 64}};
+                                 {32, 256, 1, 4, 4, 64},  {256, 192, 4, 2, 2, 64}};
 constexpr int kGemmNumCfgs = sizeof(kGemmCfgs) / sizeof(kGemmCfgs[0]);
 // A config exists for a weight format when its A and W tiles split into whole 1 KB DMA
 // instructions per wave (int8 W rows are half as wide: 128 x 160 and 128 x 96 are fp16 only).
@@ -614,10 +616,11 @@ int gemm_blocks_per_cu(int cfg, bool q8);
     HI_GEMM_CFG(4, false) HI_GEMM_CFG(5, false) HI_GEMM_CFG(6, false) HI_GEMM_CFG(7, false)                    \
     HI_GEMM_CFG(8, false) HI_GEMM_CFG(9, false) HI_GEMM_CFG(10, false) HI_GEMM_CFG(11, false)                  \
     HI_GEMM_CFG(12, false) HI_GEMM_CFG(13, false) HI_GEMM_CFG(14, false) HI_GEMM_CFG(15, false)                \
+    HI_GEMM_CFG(16, false)                                                                                     \
     HI_GEMM_CFG(0, true) HI_GEMM_CFG(1, true) HI_GEMM_CFG(2, true) HI_GEMM_CFG(3, true)                        \
     HI_GEMM_CFG(4, true) HI_GEMM_CFG(5, true) HI_GEMM_CFG(6, true) HI_GEMM_CFG(7, true)                        \
     HI_GEMM_CFG(8, true) HI_GEMM_CFG(9, true) HI_GEMM_CFG(10, true) HI_GEMM_CFG(11, true) HI_GEMM_CFG(12, true) \
-    HI_GEMM_CFG(13, true) HI_GEMM_CFG(14, true) HI_GEMM_CFG(15, true)                                          \
+    HI_GEMM_CFG(13, true) HI_GEMM_CFG(14, true) HI_GEMM_CFG(15, true) HI_GEMM_CFG(16, true)                   \
     HI_FAIL("gemm: no kernel for config %d", cfg);                                                             \
   }                                                                                                            \
   template <>                                                                                                  \
@@ -625,6 +628,6 @@ int gemm_blocks_per_cu(int cfg, bool q8);
     constexpr int EPI = EPIV;                                                                                  \
     HI_GEMM_OCC(0) HI_GEMM_OCC(1) HI_GEMM_OCC(2) HI_GEMM_OCC(3) HI_GEMM_OCC(4) HI_GEMM_OCC(5) HI_GEMM_OCC(6)    \
     HI_GEMM_OCC(7) HI_GEMM_OCC(8) HI_GEMM_OCC(9) HI_GEMM_OCC(10) HI_GEMM_OCC(11) HI_GEMM_OCC(12)              \
-    HI_GEMM_OCC(13) HI_GEMM_OCC(14) HI_GEMM_OCC(15)                                                            \
+    HI_GEMM_OCC(13) HI_GEMM_OCC(14) HI_GEMM_OCC(15) HI_GEMM_OCC(16)                                            \
     return -1;                                                                                                 \
   }

@@ -50,7 +50,7 @@ int cfg_blocks_per_cu(int cfg, bool q8) {
 
 // Relative MFMA efficiency of each tile shape (bigger tiles reuse more of what they stage).
 constexpr double kCfgEff[kGemmNumCfgs] = {0.9, 0.85, 0.85, 0.6, 0.8, 0.45, 0.4, 0.6,
-                                           1.0, 0.9, 1.05, 0.85, 0.95, 0.85, 0.8, 0.5};
+                                           1.0, 0.9, 1.05, 0.85, 0.95, 0.85, 0.8, 0.5, 0.95};
 
 struct Choice {
   int cfg, splits;
@@ -70,7 +70,7 @@ Choice gemm_pick(int M, int N, int K, bool q8, int cus) {
     const int nkt = (K + bk - 1) / bk;
     const double tiles = (double)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int slots = cus * cfg_blocks_per_cu(c, q8);
-    for (int sp = 1; sp <= 8; sp *= 2) {
+    for (int sp = 1; sp <= 8; sp += sp < 6 ? 1 : 2) {
       if (sp > nkt || (sp > 1 && tiles * sp > 4.0 * cus) || tiles > kMaxTiles) continue;
       const int kps = (nkt + sp - 1) / sp;
       const double rounds = std::ceil(tiles * sp / slots);
@@ -138,7 +138,8 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
   }
   *out = gemm_pick(g.M, g.N, g.K, q8, d->cus);
   static const bool enabled = !getenv("HIPINFER_GEMM_AUTOTUNE") || atoi(getenv("HIPINFER_GEMM_AUTOTUNE")) != 0;
-  static const bool verbose = getenv("HIPINFER_GEMM_VERBOSE") && atoi(getenv("HIPINFER_GEMM_VERBOSE")) != 0;
+  // 1: the choice per shape; 2: also every candidate's first timing
+  static const int verbose = getenv("HIPINFER_GEMM_VERBOSE") ? atoi(getenv("HIPINFER_GEMM_VERBOSE")) : 0;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   HI_TRY(hipStreamIsCapturing(s, &cap));
   if (!enabled || cap != hipStreamCaptureStatusNone) return 0;
@@ -189,11 +190,14 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
     const int nkt = (g.K + kGemmCfgs[c].bk - 1) / kGemmCfgs[c].bk;
     const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
     if (bm > 2 * mb && kGemmCfgs[c].bm != 32) continue;  // a tile far taller than M only stages padding
-    for (int sp = 1; sp <= 8 && !rc; sp *= 2) {
+    for (int sp = 1; sp <= 8 && !rc; sp += sp < 6 ? 1 : 2) {
       if (sp > nkt || (sp > 1 && tiles * sp > 4L * d->cus) || tiles > kMaxTiles) continue;
       float us = 0.f;
       rc = time_it({c, sp}, std::max(nrot, 4), &us);
       if (!rc) timed.push_back({us, {c, sp}});
+      if (!rc && verbose >= 2)
+        fprintf(stderr, "hipinfer_amd gemm autotune M=%d N=%d K=%d epi=%d%s   cfg %d (%dx%d) split %d: %.1f us\n", g.M,
+                g.N, g.K, epi, q8 ? " int8" : "", c, bm, kGemmCfgs[c].bn, sp, us);
     }
   }
   if (!rc && !timed.empty()) {

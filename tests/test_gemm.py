@@ -59,7 +59,7 @@ def gemm_check(hi, O, name, A, W, r, epi=0, bias=None, scales=None, res=None, to
 
 
 # every tile configuration (the automatic choice is -1); configs past the library's count skip
-CFGS = [-1] + list(range(16))
+CFGS = [-1] + list(range(17))
 
 
 def need_cfg(hi, cfg):
