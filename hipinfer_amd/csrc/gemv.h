@@ -49,6 +49,7 @@ struct GemvArgs {
   f16* kc;
   f16* vc;           // caches [slots][Hkv][max_seq][D]
   int max_seq, Hq, Hkv, D, kv_slot, slot_base;
+  int ipb;  // items per block per round: waves 0 .. ipb-1 of block b take items b*ipb + wave + r*grid*ipb
 };
 
 template <int WF> struct WLoad { typedef u32x4 T; };
@@ -96,7 +97,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   const int SPI = (nload + SW - 1) / SW;                // steps per item
   const int row_bytes = K * (WF == WF_F16 ? 2 : 1);
   const char* Wb = reinterpret_cast<const char*>(a.W);
-  const int nw = gridDim.x * kGemvWaves;
+  const int nw = gridDim.x * a.ipb;  // items per round
 
   // The R weight rows of item t: units t*G .. t*G+G-1 (a unit past the end repeats the last one;
   // its results are never stored).
@@ -184,7 +185,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   // ---- 2. the first step of this wave's first item
   LT wa[R][U], wb[R][U];
   Pre pa[G] = {}, pb[G] = {};
-  int t = blockIdx.x * kGemvWaves + wave, s = 0;  // the step in flight in (wa, pa)
+  int t = wave < a.ipb ? blockIdx.x * a.ipb + wave : n_items, s = 0;  // the step in flight in (wa, pa)
   issue(wa, pa, t, 0);
   // ---- 3. stage the activation rows in LDS, RMSNorm'd (HF order) when normw is given; rows >= M
   //         are zero so no garbage reaches the sums. Thread t stages chunks t, t + 512, ... of
@@ -480,8 +481,12 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   }
 }
 
-// One launch: the grid fills the resident block slots once, every wave taking the same number
-// of items (within one), so the fused-norm prologue is paid once per block.
+// One launch of k blocks per CU, each block's first ipb waves taking one item per round, (k, ipb)
+// chosen, among those that keep at least min(16, items per CU) items in flight on a CU, so that
+// the CU streaming the most items streams as few as possible (blocks b, b + CUs, ... are taken to
+// share a CU), then for the most items in flight, then for the fewest blocks (each pays the
+// activation staging once). A block's waves take consecutive items: its loads stay on
+// neighbouring rows.
 template <int MR, bool NORM, int EPI, int WF, int G>
 int gemv_launch(const GemvArgs& a, hipStream_t s) {
   const HiDevice* d = hi_device();
@@ -493,12 +498,28 @@ int gemv_launch(const GemvArgs& a, hipStream_t s) {
   if (bpc == 0) HI_FAIL("gemv: %zu bytes of activation rows do not fit in LDS", lds);
   const int n_units = EPI >= 2 ? a.N / 2 : a.N;
   const int n_items = (n_units + G - 1) / G;
-  // One item per wave while the items fit the resident slots; past that, exactly the resident
-  // blocks (bpc on every CU), the waves taking items in grid stride, so every CU streams the same
-  // share of the weights (wave counts within one item of each other).
-  const int one_each = (n_items + kGemvWaves - 1) / kGemvWaves;
-  const int grid = one_each < bpc * d->cus ? one_each : bpc * d->cus;
-  hipLaunchKernelGGL((gemv_kernel<MR, NORM, EPI, WF, G>), dim3(grid), dim3(kGemvThreads), lds, s, a);
+  const int cus = d->cus, per_cu = (n_items + cus - 1) / cus;
+  const int need = std::min(std::min(per_cu, 16), bpc * kGemvWaves);  // items in flight per CU, at least
+  int grid = 1, ipb = 1;
+  long best_load = -1;
+  int best_fly = 0;
+  for (int k = 1; k <= bpc; k++)
+    for (int w = kGemvWaves; w >= 1; w--) {
+      const long nb = n_items < cus ? n_items : (long)k * cus, nw = nb * w;
+      const long full = n_items / nw, last_blocks = (n_items - full * nw + w - 1) / w;
+      const long load = full * (nb / std::min<long>(nb, cus)) * w + (last_blocks + cus - 1) / cus * w;
+      const int fly = (int)std::min<long>((long)k * w, per_cu);
+      if (fly < need) continue;
+      if (best_load < 0 || load < best_load || (load == best_load && fly > best_fly)) {
+        best_load = load;
+        best_fly = fly;
+        grid = (int)nb;
+        ipb = w;
+      }
+    }
+  GemvArgs b = a;
+  b.ipb = ipb;
+  hipLaunchKernelGGL((gemv_kernel<MR, NORM, EPI, WF, G>), dim3(grid), dim3(kGemvThreads), lds, s, b);
   HI_TRY(hipGetLastError());
   return 0;
 }
