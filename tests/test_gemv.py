@@ -71,6 +71,28 @@ def test_gemv_epilogues(hi, O, H, I, q):
         check(f"gemv+norm+swiglu M={M} I={I}", got, O.gemv(x, gu, epi=2, normw=nw, scales=sg), 3e-3, 3e-3)
 
 
+@pytest.mark.parametrize("q", [False, True], ids=["fp16", "int8"])
+def test_every_row_written_across_grid_shapes(hi, O, q):
+    """The launch deals units to k blocks per CU with ipb items each (fewer items than CUs: one block
+    per item; partial last rounds; ipb below 8). Over unit counts that exercise each case, every
+    output row is written (the output starts as NaN) and matches the oracle."""
+    import torch
+    r = rng(7)
+    K = 256
+    for N in [1, 17, 100, 255, 256, 257, 700, 2047, 3000, 5000, 9000]:
+        for M in [1, 5]:
+            x = h16(r, M, K)
+            W = h16(r, N, K, sd=0.02)
+            s = None
+            if q:
+                W, s = q8(O, W)
+            out = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
+            hi.gemv(cuda(x), cuda(W), out=out, scales=None if s is None else cuda(s))
+            got = host(out)
+            assert np.isfinite(got.astype(np.float32)).all(), f"N={N} M={M}: rows left unwritten"
+            check(f"N={N} M={M}", got, O.gemv(x, W, scales=s), 2e-3, 2e-3)
+
+
 def test_int8_unpack_every_code_every_position(hi):
     """Each int8 code at each of the 16 byte positions of a 16-byte load (and across the 64
     lanes) comes out exactly: s = 1, x = a unit vector -> out[n] = q[n, k]."""
