@@ -101,11 +101,12 @@ __device__ __forceinline__ void store4(f16* p, f16x4 v, bool vec) {
   }
 }
 
-// Half offset of logical 16-byte chunk `c` of row `r` in an LDS tile of BK-half rows (128 or 64
-// bytes): the XOR term spreads the 16 rows one 128-bit read serves per cycle over all 64 banks.
+// Half offset of logical 16-byte chunk `c` of row `r` in an LDS tile of BK-half rows (256, 128 or
+// 64 bytes): the XOR term spreads the 16 rows one 128-bit read serves per cycle over all 64 banks.
 template <int BK>
 __device__ __forceinline__ int lds_off(int r, int c) {
-  if constexpr (BK == 64) return r * 64 + ((c ^ ((r >> 1) & 7)) << 3);
+  if constexpr (BK == 128) return r * 128 + ((c ^ (r & 15)) << 3);
+  else if constexpr (BK == 64) return r * 64 + ((c ^ ((r >> 1) & 7)) << 3);
   else return r * 32 + ((c ^ ((r >> 2) & 3)) << 3);
 }
 // Byte offset of logical 16-byte chunk `c` of row `r` in an LDS tile of BK-byte int8 rows.
@@ -148,7 +149,8 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
                     S >= 2 && S <= 8 && (S - 1) * L < 64 && 3 * L < 64,
                 "pipeline shape: every wave issues the same whole number of 1 KB DMA instructions");
   static_assert(!(GRP && Q8), "grouped (expert) GEMMs take fp16 weights");
-  static_assert(BK == 64 || BK == 32, "K tile depth");
+  static_assert(BK == 128 || BK == 64 || BK == 32, "K tile depth");
+  static_assert(BK != 128 || (!Q8 && !GRP), "128-deep K tiles take fp16 weights (and K % 128 == 0)");
   // The dynamic LDS follows the static (the split-K flag below); a 16-byte element type makes the
   // compiler start it on a 16-byte boundary, which every 128-bit LDS access and DMA here needs.
   extern __shared__ u32x4 smem_raw[];
@@ -218,15 +220,16 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   const __amdgpu_buffer_rsrc_t b_rs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<char*>(Wb + (int64_t)bn * K * (Q8 ? 1 : 2)), (short)0, (int)((int64_t)valid_n * K * (Q8 ? 1 : 2)),
       0x00020000);
-  // this lane's byte offset within an instruction's rows; the swizzle term of a 128-byte row r is
-  // ((r >> 1) & 7), which over an instruction's 8 rows depends on the instruction's parity and
-  // lane / 16; of a 64-byte row ((r >> 2) & 3) and of a 32-byte int8 row ((r >> 3) & 1), which
-  // depend on the lane only
+  // this lane's byte offset within an instruction's rows; the swizzle term of a 256-byte row r is
+  // (r & 15), which over an instruction's 4 rows depends on the instruction's index mod 4 and
+  // lane / 16; of a 128-byte row ((r >> 1) & 7), which over an instruction's 8 rows depends on the
+  // instruction's parity and lane / 16; of a 64-byte row ((r >> 2) & 3) and of a 32-byte int8 row
+  // ((r >> 3) & 1), which depend on the lane only
   const int a_r = lane / (BK / 8), a_p = lane % (BK / 8);
-  int a_lo[2], b_lo[2];
+  int a_lo[4], b_lo[4];  // per instruction index mod 4 (mod 2 for 128-byte rows; unused entries)
 #pragma unroll
-  for (int par = 0; par < 2; par++) {
-    const int sw = BK == 64 ? (par * 4 + (a_r >> 1)) & 7 : (a_r >> 2) & 3;
+  for (int par = 0; par < 4; par++) {
+    const int sw = BK == 128 ? (par * 4 + a_r) & 15 : BK == 64 ? (par * 4 + (a_r >> 1)) & 7 : (a_r >> 2) & 3;
     a_lo[par] = (int)((int64_t)a_r * g.lda * 2) + ((a_p ^ sw) << 4);
     if constexpr (Q8) {
       b_lo[par] = BK == 64 ? (lane >> 2) * K + (((lane & 3) ^ ((lane >> 4) & 3)) << 4)
@@ -242,7 +245,8 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
     for (int i = 0; i < A_LD; i++) {
       const int ri = (wave * A_LD + i) * RPI;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_void_t*)(as + ri * BK), 16,
-                                               a_lo[(ri / RPI) & 1] + (int)((int64_t)ri * g.lda * 2) + k0 * 2, 0, 0, 0);
+                                               a_lo[(ri / RPI) % (BK == 128 ? 4 : 2)] + (int)((int64_t)ri * g.lda * 2) + k0 * 2, 0, 0,
+                                               0);
     }
     char* bs = reinterpret_cast<char*>(Bs + st * B_ST);
 #pragma unroll
@@ -253,7 +257,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
       } else {
         const int ri = (wave * B_LD + i) * RPI;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rs, (lds_void_t*)(bs + ri * 2 * BK), 16,
-                                                 b_lo[(ri / RPI) & 1] + ri * K * 2 + k0 * 2, 0, 0, 0);
+                                                 b_lo[(ri / RPI) % (BK == 128 ? 4 : 2)] + ri * K * 2 + k0 * 2, 0, 0, 0);
       }
     }
   };
@@ -346,7 +350,50 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
 
   constexpr int NM = FM * FN;               // MFMAs per step
   constexpr int ND = FM + (Q8 ? 0 : FN);    // LDS reads per step (int8 W: + FN every other step)
-  if constexpr (BK == 64) {
+  if constexpr (BK == 128) {
+    // ---- 128-deep fp16 tiles (K % 128 == 0): 8 steps each, fragments one step ahead, the same
+    //      k order as two consecutive 64-deep tiles (so the same sums, bit for bit)
+    for (int t = 0; t < nloc - 1; t++) {
+      const int st = t % S;
+#pragma unroll
+      for (int p = 0; p < 3; p++) {
+        load_a(st, 2 * p + 1, af1);
+        load_b(st, 2 * p + 1, bf1);
+        mfmas(0, af0, bf0, bq0);
+        sched_step<NM, ND>();
+        load_a(st, 2 * p + 2, af0);
+        load_b(st, 2 * p + 2, bf0);
+        mfmas(0, af1, bf1, bq0);
+        sched_step<NM, ND>();
+      }
+      load_a(st, 7, af1);
+      load_b(st, 7, bf1);
+      mfmas(0, af0, bf0, bq0);
+      sched_step<NM, ND>();
+      // the tile's last fragments are in registers: free its stage, refill it, start the next tile
+      wait_lgkm0();
+      wait_vmcnt<(S - 2) * L>();
+      barrier_no_fence();
+      issue(tile_or_first(kt0 + t + S), st);
+      const int sn = (t + 1) % S;
+      load_a(sn, 0, af0);
+      load_b(sn, 0, bf0);
+      mfmas(0, af1, bf1, bq0);
+      sched_step<NM, ND>();
+    }
+    const int st = (nloc - 1) % S;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      load_a(st, 2 * p + 1, af1);
+      load_b(st, 2 * p + 1, bf1);
+      mfmas(0, af0, bf0, bq0);
+      if (p < 3) {
+        load_a(st, 2 * p + 2, af0);
+        load_b(st, 2 * p + 2, bf0);
+      }
+      mfmas(0, af1, bf1, bq0);
+    }
+  } else if constexpr (BK == 64) {
     // ---- main loop over all tiles but the last: 4 steps each, fragments one step ahead
     for (int t = 0; t < nloc - 1; t++) {
       const int st = t % S;
@@ -539,7 +586,9 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(const float* __restric
 // into exactly 256 tiles, one per CU, with no split-K. 32 x 256 (four waves side by side, 32 x 64
 // each) serves batched decode (M <= 32) on the widest projections: 32 KB of weights per stage.
 // 256 x 192 (eight waves of 64 x 96) cuts N = 3072 at M = 1024 into 64 big tiles, 256 blocks with
-// a 4-way split-K: half the staged bytes of 128 x 96 for the same K range.
+// a 4-way split-K: half the staged bytes of 128 x 96 for the same K range. The two 128-deep small
+// tiles (fp16 weights, K % 128 == 0) fetch each W row in 256-byte runs per K tile instead of
+// 128-byte ones, for the weight-streaming small-M shapes.
 struct GemmCfg {
   int bm, bn, wm, wn, st, bk;
 };
@@ -548,14 +597,19 @@ constexpr GemmCfg kGemmCfgs[] = {{256, 256, 2, 2, 2, 64}, {256, 128, 2, 2, 3, 64
                                  {32, 128, 1, 4, 4, 64},  {128, 64, 2, 2, 4, 64},  {256, 256, 2, 4, 2, 64},
                                  {256, 128, 2, 4, 3, 64}, {256, 256, 2, 4, 4, 32}, {256, 128, 2, 2, 6, 32},
                                  {128, 256, 2, 4, 6, 32}, {128, 160, 4, 1, 4, 64}, {128, 96, 4, 1, 4, 64},
-                                 {32, 256, 1, 4, 4, 64},  {256, 192, 4, 2, 2, 64}};
+                                 {32, 256, 1, 4, 4, 64},  {256, 192, 4, 2, 2, 64}, {64, 128, 2, 2, 3, 128},
+                                 {128, 64, 2, 2, 3, 128}};
 constexpr int kGemmNumCfgs = sizeof(kGemmCfgs) / sizeof(kGemmCfgs[0]);
 // A config exists for a weight format when its A and W tiles split into whole 1 KB DMA
 // instructions per wave (int8 W rows are half as wide: 128 x 160 and 128 x 96 are fp16 only).
 constexpr bool gemm_cfg_ok(int c, bool q8) {
   const int nw = kGemmCfgs[c].wm * kGemmCfgs[c].wn, bk = kGemmCfgs[c].bk;
   const int a = kGemmCfgs[c].bm * 2 * bk, b = kGemmCfgs[c].bn * (q8 ? bk : 2 * bk);
-  return a % (1024 * nw) == 0 && b % (1024 * nw) == 0 && a >= 1024 * nw && b >= 1024 * nw;
+  return a % (1024 * nw) == 0 && b % (1024 * nw) == 0 && a >= 1024 * nw && b >= 1024 * nw && !(q8 && bk == 128);
+}
+// ... and for a shape: 128-deep tiles have no K tail, so they need K % 128 == 0.
+constexpr bool gemm_cfg_fits(int c, bool q8, int K) {
+  return gemm_cfg_ok(c, q8) && (kGemmCfgs[c].bk < 128 || K % 128 == 0);
 }
 constexpr int kGemmGrpCfg = 3;  // the grouped (MoE expert) GEMM's tile: 64 x 128
 inline size_t gemm_lds_bytes(int cfg, bool q8) {
@@ -616,7 +670,7 @@ int gemm_blocks_per_cu(int cfg, bool q8);
     HI_GEMM_CFG(4, false) HI_GEMM_CFG(5, false) HI_GEMM_CFG(6, false) HI_GEMM_CFG(7, false)                    \
     HI_GEMM_CFG(8, false) HI_GEMM_CFG(9, false) HI_GEMM_CFG(10, false) HI_GEMM_CFG(11, false)                  \
     HI_GEMM_CFG(12, false) HI_GEMM_CFG(13, false) HI_GEMM_CFG(14, false) HI_GEMM_CFG(15, false)                \
-    HI_GEMM_CFG(16, false)                                                                                     \
+    HI_GEMM_CFG(16, false) HI_GEMM_CFG(17, false) HI_GEMM_CFG(18, false)                                       \
     HI_GEMM_CFG(0, true) HI_GEMM_CFG(1, true) HI_GEMM_CFG(2, true) HI_GEMM_CFG(3, true)                        \
     HI_GEMM_CFG(4, true) HI_GEMM_CFG(5, true) HI_GEMM_CFG(6, true) HI_GEMM_CFG(7, true)                        \
     HI_GEMM_CFG(8, true) HI_GEMM_CFG(9, true) HI_GEMM_CFG(10, true) HI_GEMM_CFG(11, true) HI_GEMM_CFG(12, true) \
@@ -628,6 +682,6 @@ int gemm_blocks_per_cu(int cfg, bool q8);
     constexpr int EPI = EPIV;                                                                                  \
     HI_GEMM_OCC(0) HI_GEMM_OCC(1) HI_GEMM_OCC(2) HI_GEMM_OCC(3) HI_GEMM_OCC(4) HI_GEMM_OCC(5) HI_GEMM_OCC(6)    \
     HI_GEMM_OCC(7) HI_GEMM_OCC(8) HI_GEMM_OCC(9) HI_GEMM_OCC(10) HI_GEMM_OCC(11) HI_GEMM_OCC(12)              \
-    HI_GEMM_OCC(13) HI_GEMM_OCC(14) HI_GEMM_OCC(15) HI_GEMM_OCC(16)                                            \
+    HI_GEMM_OCC(13) HI_GEMM_OCC(14) HI_GEMM_OCC(15) HI_GEMM_OCC(16) HI_GEMM_OCC(17) HI_GEMM_OCC(18)            \
     return -1;                                                                                                 \
   }

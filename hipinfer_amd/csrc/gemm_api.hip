@@ -50,7 +50,7 @@ int cfg_blocks_per_cu(int cfg, bool q8) {
 
 // Relative MFMA efficiency of each tile shape (bigger tiles reuse more of what they stage).
 constexpr double kCfgEff[kGemmNumCfgs] = {0.9, 0.85, 0.85, 0.6, 0.8, 0.45, 0.4, 0.6,
-                                           1.0, 0.9, 1.05, 0.85, 0.95, 0.85, 0.8, 0.5, 0.95};
+                                           1.0, 0.9, 1.05, 0.85, 0.95, 0.85, 0.8, 0.5, 0.95, 0.6, 0.6};
 
 struct Choice {
   int cfg, splits;
@@ -65,7 +65,7 @@ Choice gemm_pick(int M, int N, int K, bool q8, int cus) {
   const double mfma_per_cu = 4069.0 * 2.4e9;  // fp16 flop/s per CU at the datasheet peak
   const double l2_bw = 20e12;                 // aggregate L2/MALL bytes/s the staging can draw
   for (int c = 0; c < kGemmNumCfgs; c++) {
-    if (!gemm_cfg_ok(c, q8)) continue;
+    if (!gemm_cfg_fits(c, q8, K)) continue;
     const int bm = kGemmCfgs[c].bm, bn = kGemmCfgs[c].bn, bk = kGemmCfgs[c].bk;
     const int nkt = (K + bk - 1) / bk;
     const double tiles = (double)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
@@ -185,7 +185,7 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
   std::vector<std::pair<float, Choice>> timed;
   int rc = 0;
   for (int c = 0; c < kGemmNumCfgs && !rc; c++) {
-    if (!gemm_cfg_ok(c, q8)) continue;
+    if (!gemm_cfg_fits(c, q8, g.K)) continue;
     const int bm = kGemmCfgs[c].bm, bn = kGemmCfgs[c].bn;
     const int nkt = (g.K + kGemmCfgs[c].bk - 1) / kGemmCfgs[c].bk;
     const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
@@ -294,7 +294,7 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
   g.K = K;
   g.vec_c = aligned(C, 8) && ldc % 4 == 0;
   Choice ch{1, 1};
-  if (g_force_cfg >= 0 && g_force_cfg < kGemmNumCfgs && gemm_cfg_ok(g_force_cfg, q8)) {  // else: automatic
+  if (g_force_cfg >= 0 && g_force_cfg < kGemmNumCfgs && gemm_cfg_fits(g_force_cfg, q8, K)) {  // else: automatic
     ch = gemm_pick(M, N, K, q8, d->cus);
     ch.cfg = g_force_cfg;
   } else if (int r = gemm_choose(g, epi, q8, s, &ch)) {
