@@ -509,14 +509,14 @@ def moe_bench(torch, hi, steps, seed):
             x.copy_(x0)
             for l in range(L):
                 if path < 0:  # router + experts in one call
-                    hi.lib.hi_moe_route_experts(hi._p(xn), xn.stride(0), hi._p(Wr[l]), hi._p(wgu[l]), hi._p(wdn[l]), M,
-                                                E, k, H, I, flags, 0.22, hi._p(x), x.stride(0), hi._p(idx),
-                                                hi._p(wts), hi._p(work), hi._s())
+                    hi.lib.hi_moe_route_experts(hi.ptr(xn), xn.stride(0), hi.ptr(Wr[l]), hi.ptr(wgu[l]), hi.ptr(wdn[l]), M,
+                                                E, k, H, I, flags, 0.22, hi.ptr(x), x.stride(0), hi.ptr(idx),
+                                                hi.ptr(wts), hi.ptr(work), hi.cur_stream())
                     continue
-                hi.lib.hi_moe_router(hi._p(xn), xn.stride(0), hi._p(Wr[l]), M, E, H, k, flags, hi._p(idx), hi._p(wts),
-                                     hi._s())
-                hi.lib.hi_moe_experts(hi._p(xn), xn.stride(0), hi._p(wgu[l]), hi._p(wdn[l]), hi._p(idx), hi._p(wts), M,
-                                      E, k, H, I, flags, 0.22, hi._p(x), x.stride(0), path, hi._p(work), hi._s())
+                hi.lib.hi_moe_router(hi.ptr(xn), xn.stride(0), hi.ptr(Wr[l]), M, E, H, k, flags, hi.ptr(idx), hi.ptr(wts),
+                                     hi.cur_stream())
+                hi.lib.hi_moe_experts(hi.ptr(xn), xn.stride(0), hi.ptr(wgu[l]), hi.ptr(wdn[l]), hi.ptr(idx), hi.ptr(wts), M,
+                                      E, k, H, I, flags, 0.22, hi.ptr(x), x.stride(0), path, hi.ptr(work), hi.cur_stream())
         ms = _time(torch, step, steps)
         us = ms * 1e3 / L
         if M == 1:

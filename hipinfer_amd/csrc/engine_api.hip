@@ -33,7 +33,10 @@
 namespace {
 
 constexpr int32_t kMagic = 0x48495046;
-constexpr int kVerifyMaxRows = 8;  // rows per verify: the GEMV path's fused-norm limit
+// rows per verify (k + 1 for k draft tokens), the reference's kGemvMaxRows (api.cu:156). The GEMV
+// host runs fused-norm launches of at most 8 rows, so 9..16 rows take two launches per projection;
+// a row's arithmetic does not depend on the launch it is in.
+constexpr int kVerifyMaxRows = 16;
 
 struct Cfg {
   int vocab = 0, hidden = 0, inter = 0, layers = 0, heads = 0, kv = 0, head_dim = 0, max_pos = 0, window = 0;
@@ -137,12 +140,6 @@ void free_engine(Engine* e) {
   for (void* p : e->allocs) (void)hipFree(p);
   if (e->st) (void)hipStreamDestroy(e->st);
   delete e;
-}
-
-int env_gemv_max() {
-  const char* v = getenv("HIPINFER_GEMV_MAX");
-  const int n = v ? atoi(v) : 8;
-  return n < 0 ? 0 : n > 8 ? 8 : n;
 }
 
 // Stream file bytes [from, to) into dst through two pinned staging buffers.
@@ -470,7 +467,7 @@ Engine* load(const char* path, int maxB, int max_seq, int max_pf) {
     return fail();
   }
   if (hipStreamCreate(&e->st) != hipSuccess) return fail();
-  e->maxB = maxB, e->max_seq = max_seq, e->max_pf = max_pf, e->gemv_max = env_gemv_max();
+  e->maxB = maxB, e->max_seq = max_seq, e->max_pf = max_pf, e->gemv_max = hi_gemv_max_rows();
   const int H = c.hidden, D = c.head_dim, Hq = c.heads, Hkv = c.kv, I = c.inter, V = c.vocab;
   e->qkv_dim = (Hq + 2 * Hkv) * D;
   std::vector<float> inv(D / 2);
@@ -734,6 +731,10 @@ HI_EXPORT int hi_verify(Engine* e, int slot, const int* tokens, int R, int p0, i
                         int use_graph) {
   if (!e || e->c.moe) {
     fprintf(stderr, "hi_verify: dense models only\n");
+    return -1;
+  }
+  if (e->gemv_max < 1) {
+    fprintf(stderr, "hi_verify: a batch of one must decode on the GEMV path (HIPINFER_GEMV_MAX >= 1)\n");
     return -1;
   }
   if (R < 1 || R > kVerifyMaxRows || !out) {

@@ -55,6 +55,7 @@ constexpr double kCfgEff[kGemmNumCfgs] = {0.9, 0.85, 0.85, 0.6, 0.8, 0.45, 0.4, 
 struct Choice {
   int cfg, splits;
 };
+thread_local Choice g_last{-1, 0};  // the (tile, split) of this thread's last launch (hi_gemm_last_choice)
 
 // Fallback model (stream capture, autotuning off): rounds of resident blocks times the tile's
 // MFMA time at its efficiency, or the L2/MALL time of everything the tiles stage, whichever is
@@ -256,6 +257,7 @@ int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s
     }
   }
   g.kt_per_split = kps;
+  g_last = ch;
   switch (epi) {
     case 0: return gemm_run<0>(g, ch.cfg, ch.splits, q8, s);
     case 1: return gemm_run<1>(g, ch.cfg, ch.splits, q8, s);
@@ -330,6 +332,14 @@ HI_EXPORT int hi_gemm_force_splits(int sp) {
   return 0;
 }
 HI_EXPORT int hi_gemm_num_configs() { return kGemmNumCfgs; }
+// Test hook: the tile config and split count the calling thread's last hi_gemm / hi_gemm_w8 launch
+// ran with (after a forced config that does not fit fell back to the automatic choice, and splits
+// were capped to the K tiles); -1 and 0 before any launch.
+HI_EXPORT int hi_gemm_last_choice(int* cfg, int* splits) {
+  if (cfg) *cfg = g_last.cfg;
+  if (splits) *splits = g_last.splits;
+  return 0;
+}
 HI_EXPORT int hi_gemm_config_desc(int c, char* out, int n) {
   if (c < 0 || c >= kGemmNumCfgs || !out || n < 1) return -1;
   snprintf(out, n, "mfma 32x32x16 %dx%dx%d waves %dx%d stages %d", kGemmCfgs[c].bm, kGemmCfgs[c].bn, kGemmCfgs[c].bk,

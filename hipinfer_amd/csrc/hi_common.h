@@ -48,6 +48,11 @@ const HiDevice* hi_device();  // current device; nullptr on a HIP error (already
 // Largest number of resident blocks of `fn` per CU at `block` threads and `lds` dynamic bytes
 // (cached per device and kernel); sets the kernel's dynamic-LDS limit first when lds > 64 KB.
 int hi_blocks_per_cu(const void* fn, int block, size_t lds);
+// HIPINFER_GEMV_MAX (default 8, clamped to 0..8): the largest batch the decode step and the MoE
+// experts run on the GEMV path; larger batches take the GEMM path. One value for both callers, as
+// in the reference (api.cu:1884-1887), whose default is 4: on MI355X the GEMV stays ahead of the
+// small-M GEMM tiles through 8 rows. Read once per process.
+int hi_gemv_max_rows();
 
 // ------------------------------------------------------------------ device helpers
 // DPP lane moves with compile-time controls (gfx9 encodings): quad_perm, row_half_mirror, row_mirror.

@@ -7,6 +7,7 @@
 // hi_rmsnorm is the unfused form of the GEMV prologue (reference api.cu hi_rmsnorm,
 // kernels.cuh:110-125), kept because the reference's fused-QKV tests build their expected values
 // from it.
+#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -76,6 +77,15 @@ int hi_blocks_per_cu(const void* fn, int block, size_t lds) {
   std::lock_guard<std::mutex> lk(g_mu);
   cache[key] = n;
   return n;
+}
+
+int hi_gemv_max_rows() {
+  static const int v = [] {
+    const char* e = getenv("HIPINFER_GEMV_MAX");
+    const int n = e ? atoi(e) : 8;
+    return n < 0 ? 0 : n > 8 ? 8 : n;
+  }();
+  return v;
 }
 
 HI_EXPORT int hi_device_cus() {

@@ -439,12 +439,8 @@ int grouped_gemm(const f16* A, int lda, const f16* W, int64_t wstride_bytes, f16
 
 size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 
-// HIPINFER_GEMV_MAX (default 4, at most 8): the largest row count the GEMV path takes
-// (reference api.cu:1884-1887).
-int gemv_max() {
-  static const int v = getenv("HIPINFER_GEMV_MAX") ? atoi(getenv("HIPINFER_GEMV_MAX")) : 4;
-  return v < 8 ? v : 8;
-}
+// The largest row count the GEMV path takes: HIPINFER_GEMV_MAX, shared with the decode step.
+int gemv_max() { return hi_gemv_max_rows(); }
 
 // The expert workspace (hi_moe_work_bytes), each piece on a 256-byte boundary.
 struct MoeWork {
@@ -504,7 +500,7 @@ HI_EXPORT size_t hi_moe_work_bytes(int M, int k, int E, int H, int I) {
 
 // x[m] += MoE(xn[m]) for M rows given the routing (idx, w from hi_moe_router): wgu [E][2I, H]
 // (gate/up interleaved per expert), wdown [E][H, I]. path 0 takes the GEMV path for
-// M <= HIPINFER_GEMV_MAX (default 4), else the grouped path; 1 / 2 force GEMV / grouped.
+// M <= HIPINFER_GEMV_MAX (default 8), else the grouped path; 1 / 2 force GEMV / grouped.
 HI_EXPORT int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const void* wdown, const int* idx, const float* w,
                              int M, int E, int k, int H, int I, int flags, float scale, void* x, int ldx, int path,
                              void* work, void* s) {

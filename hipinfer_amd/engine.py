@@ -31,14 +31,16 @@ eager step:
     logits = RMSNorm(x; nf) @ Wlm^T
     tok = argmax(logits); pos += 1                                (greedy, kernels.cuh:1913-1931)
 
-The weight-file loader that the reference's hi_load adds around this is not part of this
-package; a caller supplies the weights.
+This class takes weights already in device memory (tests and benchmarks build them from seeds).
+The weight-file path is the library's own engine (csrc/engine_api.hip: hi_load, hi_prefill,
+hi_decode, hi_verify), which runs the same kernels in the same order and which hipinfer.Engine
+wraps.
 """
 import torch
 
 from . import hipinfer as hi
 
-GEMV_MAX = 8  # sequences per decode step on the GEMV path (the reference's HIPINFER_GEMV_MAX cap)
+GEMV_MAX = 8  # sequences per decode step on the GEMV path (the library's HIPINFER_GEMV_MAX default)
 GEMM_MAX = 64  # and on the batched-decode GEMM path
 
 

@@ -1,412 +1,530 @@
-"""ctypes host for libhipinfer.so: the matmul hot path of hipinfer on torch tensors.
+"""Python face of libhipinfer.so: the hipinfer matmul hot path (and the engine built on it) called
+on torch tensors that live on an MI355X.
 
-Mirrors the kernel-level functions of the reference's scripts/hipinfer.py (gemv, gemv_qkv_rope,
-gemm, moe_router, moe_experts, rmsnorm, decode_attn; hipinfer.py:101-190, 288-306) with the same names,
-arguments and defaults, over the same hi_* C symbols, plus the int8 quantiser of
-scripts/export.py:54-101 (quantize_rows, dequantize_rows, interleave_gate_up) running on the GPU.
-torch is only the container for device memory and the current stream.
+The public names, argument order, defaults and return values are those of the reference's
+Python module (scripts/hipinfer.py: rmsnorm, gemv, gemv_qkv_rope, gemm, moe_router, moe_experts,
+decode_attn, rope_cache, flash_prefill, flash_prefill_lse, Engine), so code written against it
+runs here unchanged; the int8 weight tools of scripts/export.py:54-101 (quantize_rows,
+dequantize_rows, interleave_gate_up) are here too, the first two running on the GPU.
 
-Errors: a launcher that rejects its arguments returns a negative code (the reason is printed on
-stderr); these wrappers raise ValueError then. There is no CPU fallback: without the built library
-or a GPU every call fails.
+How this module is put together:
+  * the C-ABI is declared once, below, as C prototypes (the same text as include/hipinfer.h);
+    a small parser turns each prototype into ctypes argtypes / restype, and a CPU test checks the
+    table against the header, so the two cannot drift apart;
+  * every wrapper validates its tensors (device, dtype, rank, row layout) before any launch, then
+    makes one C call on torch's current stream; a non-zero code from the library (it prints the
+    reason on stderr) becomes ValueError;
+  * torch only provides device memory and the stream: there is no CPU path. Importing fails when
+    the library is not built, and every call needs the GPU.
 """
-import ctypes as C
+import ctypes
 import os
+import re
 
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB = os.environ.get("HIPINFER_LIB", os.path.join(_HERE, "libhipinfer.so"))
-if not os.path.exists(_LIB):
-    raise ImportError(f"hipinfer_amd: {_LIB} is not built; run `python -m hipinfer_amd.build`")
-lib = C.CDLL(os.path.abspath(_LIB))
+LIBRARY_PATH = os.path.abspath(os.environ.get("HIPINFER_LIB", os.path.join(_HERE, "libhipinfer.so")))
+if not os.path.exists(LIBRARY_PATH):
+    raise ImportError(f"hipinfer_amd: {LIBRARY_PATH} is not built; run `python -m hipinfer_amd.build`")
+lib = ctypes.CDLL(LIBRARY_PATH)
 
-P, I, F, LL = C.c_void_p, C.c_int, C.c_float, C.c_longlong
-_SIGS = {
-    "hi_rmsnorm": [P, P, P, I, I, F, P],
-    "hi_gemv": [P, I, P, F, P, P, I, I, I, I, I, P],
-    "hi_gemv_w8": [P, I, P, F, P, P, P, I, I, I, I, I, P],
-    "hi_gemv_qkv_rope": [P, I, P, F, P, P, P, I, I, I, I, I, I, P, P, P, P, I, P],
-    "hi_gemv_qkv_rope_w8": [P, I, P, F, P, P, P, P, I, I, I, I, I, I, P, P, P, P, I, P],
-    "hi_quantize_rows": [P, LL, I, P, P, P],
-    "hi_dequantize_rows": [P, P, LL, I, P, P],
-    "hi_device_cus": [],
-}
-_OPTIONAL = {
-    "hi_gemm": [P, I, P, P, P, I, I, I, I, I, P],
-    "hi_gemm_w8": [P, I, P, P, P, P, I, I, I, I, I, P],
-    "hi_gemm_force_config": [I],
-    "hi_gemm_force_splits": [I],
-    "hi_gemm_num_configs": [],
-    "hi_gemm_config_desc": [I, C.c_char_p, I],
-    "hi_moe_router": [P, I, P, I, I, I, I, I, P, P, P],
-    "hi_moe_work_bytes": [I, I, I, I, I],
-    "hi_moe_experts": [P, I, P, P, P, P, I, I, I, I, I, I, F, P, I, I, P, P],
-    "hi_moe_route_experts": [P, I, P, P, P, I, I, I, I, I, I, F, P, I, P, P, P, P],
-    "hi_decode_work_bytes": [I, I, I, I],
-    "hi_decode_attn": [P, I, P, P, I, P, P, I, I, I, I, I, P, P],
-    "hi_argmax": [P, I, I, P, P],
-    "hi_embed": [P, P, I, I, P, I, I, P],
-    "hi_rope_cache": [P, I, I, I, I, I, P, P, I, I, P, P, I, P],
-    "hi_flash_prefill": [P, I, P, P, I, P, I, I, I, I, I, I, P],
-    "hi_flash_prefill_lse": [P, I, P, P, I, P, I, I, I, I, I, I, P, P],
-    # engine (one GPU)
-    "hi_load": [C.c_char_p, I, I, I],
-    "hi_load_tp": [C.c_char_p, I, I, I, I, P],
-    "hi_free": [P],
-    "hi_config": [P, P],
-    "hi_moe_config": [P, P],
-    "hi_weight_bytes": [P],
-    "hi_weight_quant": [P],
-    "hi_prefill": [P, I, P, I, I],
-    "hi_prefill_logits": [P, I, P, I, I, P],
-    "hi_decode": [P, I, I, I],
-    "hi_history": [P, I, I, I, P],
-    "hi_logits": [P, I, P],
-    "hi_set_state": [P, I, P, P],
-    "hi_rewind": [P, I, I, I],
-    "hi_sync": [P],
-    "hi_stream": [P],
-    "hi_verify_max_rows": [],
-    "hi_verify": [P, I, P, I, I, P, P, I],
-}
-for _name, _args in list(_SIGS.items()) + [(n, a) for n, a in _OPTIONAL.items() if hasattr(lib, n)]:
-    _fn = getattr(lib, _name)
-    _fn.argtypes = _args
-    _fn.restype = I
-for _name, _rt in [("hi_moe_work_bytes", C.c_size_t), ("hi_decode_work_bytes", C.c_size_t),
-                   ("hi_weight_bytes", C.c_size_t), ("hi_load", P), ("hi_load_tp", P), ("hi_decode", F),
-                   ("hi_stream", P), ("hi_free", None), ("hi_config", None), ("hi_moe_config", None), ("hi_sync", None)]:
-    if hasattr(lib, _name):
-        getattr(lib, _name).restype = _rt
-MOE_NORM_TOPK, MOE_FP16_WEIGHTS = 1, 2  # moe_flags bits (reference scripts/hipinfer.py:67)
+# moe_flags bits (the reference's MOE_NORM_TOPK / MOE_FP16_WEIGHTS): softmax over the chosen k
+# instead of all experts; routing weights rounded to fp16.
+MOE_NORM_TOPK = 1
+MOE_FP16_WEIGHTS = 2
 
+# ------------------------------------------------------------------ the C-ABI, as prototypes
+ABI = """
+int hi_rmsnorm(ptr x, ptr w, ptr y, int M, int H, float eps, ptr stream);
+int hi_gemv(ptr x, int ldx, ptr normw, float eps, ptr W, ptr out, int ldo, int M, int N, int K, int epi, ptr stream);
+int hi_gemv_w8(ptr x, int ldx, ptr normw, float eps, ptr W, ptr scales, ptr out, int ldo, int M, int N, int K,
+               int epi, ptr stream);
+int hi_gemv_qkv_rope(ptr x, int ldx, ptr normw, float eps, ptr W, ptr bias, ptr out, int ldo, int M, int K, int Hq,
+                     int Hkv, int D, ptr cs, ptr pos, ptr kc, ptr vc, int max_seq, ptr stream);
+int hi_gemv_qkv_rope_w8(ptr x, int ldx, ptr normw, float eps, ptr W, ptr scales, ptr bias, ptr out, int ldo, int M,
+                        int K, int Hq, int Hkv, int D, ptr cs, ptr pos, ptr kc, ptr vc, int max_seq, ptr stream);
+int hi_quantize_rows(ptr w, i64 N, int K, ptr q, ptr s, ptr stream);
+int hi_dequantize_rows(ptr q, ptr s, i64 N, int K, ptr out, ptr stream);
+int hi_device_cus();
+int hi_gemm(ptr A, int lda, ptr W, ptr bias, ptr C, int ldc, int M, int N, int K, int epi, ptr stream);
+int hi_gemm_w8(ptr A, int lda, ptr W, ptr scales, ptr bias, ptr C, int ldc, int M, int N, int K, int epi, ptr stream);
+int hi_gemm_force_config(int cfg);
+int hi_gemm_force_splits(int splits);
+int hi_gemm_num_configs();
+int hi_gemm_config_desc(int cfg, str out, int n);
+int hi_gemm_last_choice(ptr cfg, ptr splits);
+int hi_moe_router(ptr xn, int ldx, ptr Wr, int M, int E, int H, int k, int flags, ptr idx, ptr w, ptr stream);
+size hi_moe_work_bytes(int M, int k, int E, int H, int I);
+int hi_moe_experts(ptr xn, int ldxn, ptr wgu, ptr wdown, ptr idx, ptr w, int M, int E, int k, int H, int I, int flags,
+                   float scale, ptr x, int ldx, int path, ptr work, ptr stream);
+int hi_moe_route_experts(ptr xn, int ldxn, ptr Wr, ptr wgu, ptr wdown, int M, int E, int k, int H, int I, int flags,
+                         float scale, ptr x, int ldx, ptr idx, ptr w, ptr work, ptr stream);
+size hi_decode_work_bytes(int B, int Hq, int Hkv, int D);
+int hi_decode_attn(ptr q, int ldq, ptr kc, ptr vc, int max_seq, ptr pos, ptr out, int ldo, int B, int Hq, int Hkv,
+                   int D, ptr work, ptr stream);
+int hi_argmax(ptr logits, int B, int V, ptr tok, ptr stream);
+int hi_embed(ptr tok, ptr table, int V, int H, ptr x, int ldx, int B, ptr stream);
+int hi_rope_cache(ptr qkv, int ldq, int M, int Hq, int Hkv, int D, ptr cs, ptr pos, int pos_base, int slot_base,
+                  ptr kc, ptr vc, int max_seq, ptr stream);
+int hi_flash_prefill(ptr q, int ldq, ptr kc, ptr vc, int max_seq, ptr out, int ldo, int T, int p0, int Hq, int Hkv,
+                     int D, ptr stream);
+int hi_flash_prefill_lse(ptr q, int ldq, ptr kc, ptr vc, int max_seq, ptr out, int ldo, int T, int p0, int Hq,
+                         int Hkv, int D, ptr lse, ptr stream);
+ptr hi_load(str path, int max_batch, int max_seq, int max_prefill);
+ptr hi_load_tp(str path, int max_batch, int max_seq, int max_prefill, int world, ptr devs);
+void hi_free(ptr e);
+void hi_config(ptr e, ptr out);
+void hi_moe_config(ptr e, ptr out);
+size hi_weight_bytes(ptr e);
+int hi_weight_quant(ptr e);
+int hi_prefill(ptr e, int slot, ptr tokens, int T, int p0);
+int hi_prefill_logits(ptr e, int slot, ptr tokens, int T, int p0, ptr logits);
+float hi_decode(ptr e, int B, int steps, int use_graph);
+int hi_history(ptr e, int slot, int start, int n, ptr out);
+int hi_logits(ptr e, int B, ptr out);
+int hi_set_state(ptr e, int B, ptr tokens, ptr positions);
+int hi_rewind(ptr e, int slot, int len, int tok);
+void hi_sync(ptr e);
+ptr hi_stream(ptr e);
+int hi_verify_max_rows();
+int hi_verify(ptr e, int slot, ptr tokens, int R, int p0, ptr out, ptr logits, int use_graph);
+"""
 
-def _s():
-    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
-
-
-def _p(t):
-    return C.c_void_p(t.data_ptr()) if t is not None else None
+_CTYPE = {"int": ctypes.c_int, "i64": ctypes.c_longlong, "float": ctypes.c_float, "size": ctypes.c_size_t,
+          "ptr": ctypes.c_void_p, "str": ctypes.c_char_p, "void": None}
 
 
-def _ok(r, what):
-    if r != 0:
-        raise ValueError(f"hipinfer_amd {what}: rejected (code {r}; reason on stderr)")
+def parse_abi(text):
+    """{name: (return kind, [argument kinds])} from prototypes `kind name(kind arg, ...);`."""
+    decls = {}
+    for m in re.finditer(r"(\w+)\s+(hi_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = [a.split()[0] for a in m.group(3).split(",") if a.strip()]
+        decls[m.group(2)] = (m.group(1), args)
+    return decls
 
 
-def _dev(*ts):
-    for t in ts:
-        if t is not None and not t.is_cuda:
-            raise ValueError("hipinfer_amd: tensors must live on the GPU")
+SIGNATURES = parse_abi(ABI)
+for _name, (_ret, _args) in SIGNATURES.items():
+    _fn = getattr(lib, _name)  # every prototype must exist in the library
+    _fn.restype = _CTYPE[_ret]
+    _fn.argtypes = [_CTYPE[a] for a in _args]
 
 
-# W [N, K]: fp16, or int8 with `scales` [N] fp16 (one per output row: W ~ W_int8 * scales[:, None]).
-def _w8(W, scales):
+# ------------------------------------------------------------------ call helpers
+def ptr(t):
+    """Device address of a tensor (None passes NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def cur_stream():
+    """torch's current HIP stream, as the library's `stream` argument."""
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def check_rc(rc, what):
+    """A library return code: 0 is success; the library printed the reason for anything else."""
+    if rc != 0:
+        raise ValueError(f"hipinfer_amd.{what}: the library rejected the call (code {rc}; reason on stderr)")
+    return rc
+
+
+def _need(what, t, dtype=None, ndim=None, rows=False, optional=False):
+    """Checks one tensor argument: on a GPU, of the given dtype and rank; rows=True also needs unit
+    stride along the last dimension (rows may be strided, as leading dimensions allow)."""
+    if t is None:
+        if optional:
+            return
+        raise ValueError(f"hipinfer_amd.{what}: a tensor argument is missing")
+    if not t.is_cuda:
+        raise ValueError(f"hipinfer_amd.{what}: tensors must live on the GPU (got {t.device})")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"hipinfer_amd.{what}: expected {dtype}, got {t.dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"hipinfer_amd.{what}: expected {ndim} dimensions, got shape {tuple(t.shape)}")
+    if rows and t.stride(-1) != 1:
+        raise ValueError(f"hipinfer_amd.{what}: rows must be contiguous")
+
+
+def _weight(what, W, scales):
+    """A [N, K] projection: fp16, or int8 with one fp16 scale per row. Returns True for int8."""
+    _need(what, W, ndim=2, rows=True)
     if scales is None:
-        assert W.dtype == torch.float16
+        if W.dtype != torch.float16:
+            raise ValueError(f"hipinfer_amd.{what}: fp16 weights, or int8 weights with scales")
         return False
-    assert W.dtype == torch.int8 and scales.dtype == torch.float16 and scales.shape == (W.shape[0],)
+    _need(what, scales, torch.float16, 1)
+    if W.dtype != torch.int8 or scales.shape[0] != W.shape[0]:
+        raise ValueError(f"hipinfer_amd.{what}: int8 weights need one fp16 scale per row")
     return True
 
 
+def _alloc_rows(ref, M, N, dtype=torch.float16):
+    return torch.empty(M, N, dtype=dtype, device=ref.device)
+
+
+# ------------------------------------------------------------------ kernels
 def rmsnorm(x, w, eps=1e-5, out=None):
-    """y = w * fp16(x * rsqrt(mean(x^2) + eps)) per row of x [M, H] (contiguous rows)."""
+    """RMSNorm of each row of x [M, H]: w * fp16(x * rsqrt(mean(x^2) + eps)), HF rounding order."""
     y = torch.empty_like(x) if out is None else out
-    _dev(x, w, y)
+    for t in (x, w, y):
+        _need("rmsnorm", t, torch.float16)
     if not (x.is_contiguous() and y.is_contiguous()):
-        raise ValueError("hipinfer_amd: rmsnorm rows must be contiguous")
-    _ok(lib.hi_rmsnorm(_p(x), _p(w), _p(y), x.shape[0], x.shape[1], eps, _s()), "rmsnorm")
+        raise ValueError("hipinfer_amd.rmsnorm: rows of x and out must be packed")
+    check_rc(lib.hi_rmsnorm(ptr(x), ptr(w), ptr(y), x.shape[0], x.shape[1], eps, cur_stream()), "rmsnorm")
     return y
 
 
 def gemv(x, W, out=None, normw=None, eps=1e-5, epi=0, scales=None):
-    """out[M, *] (epi) x[M, K] @ W[N, K]^T for small M; epi 0 store, 1 residual (out += y),
-    2 SwiGLU over gate/up rows interleaved in groups of 16 (out is N/2 wide)."""
+    """Decode GEMV for a few activation rows x [M, K] against W [N, K]:
+    epi 0 writes x W^T, epi 1 adds it to out (residual), epi 2 writes the SwiGLU of gate/up row pairs
+    (W's rows interleaved in groups of 16; out is N/2 wide). normw fuses an RMSNorm of x first."""
+    _need("gemv", x, torch.float16, 2, rows=True)
+    q8 = _weight("gemv", W, scales)
+    _need("gemv", normw, torch.float16, 1, optional=True)
     M, K = x.shape
     N = W.shape[0]
     if out is None:
-        out = torch.empty(M, N // 2 if epi == 2 else N, dtype=x.dtype, device=x.device)
-    _dev(x, W, out, normw, scales)
-    if _w8(W, scales):
-        r = lib.hi_gemv_w8(_p(x), x.stride(0), _p(normw), eps, _p(W), _p(scales), _p(out), out.stride(0), M, N, K, epi,
-                           _s())
-    else:
-        r = lib.hi_gemv(_p(x), x.stride(0), _p(normw), eps, _p(W), _p(out), out.stride(0), M, N, K, epi, _s())
-    _ok(r, "gemv")
+        out = _alloc_rows(x, M, N // 2 if epi == 2 else N)
+    _need("gemv", out, torch.float16, 2, rows=True)
+    head = (ptr(x), x.stride(0), ptr(normw), eps, ptr(W))
+    tail = (ptr(out), out.stride(0), M, N, K, epi, cur_stream())
+    rc = lib.hi_gemv_w8(*head, ptr(scales), *tail) if q8 else lib.hi_gemv(*head, *tail)
+    check_rc(rc, "gemv")
     return out
 
 
 def gemv_qkv_rope(x, W, normw, Hq, Hkv, cs, pos, kc, vc, out, bias=None, eps=1e-5, scales=None):
-    """Fused RMSNorm + QKV GEMV (+ bias) + RoPE + KV-cache write. Row m -> cache slot m at pos[m]."""
-    D = kc.shape[-1]
-    _dev(x, W, cs, pos, kc, vc, out, bias, normw, scales)
-    if _w8(W, scales):
-        r = lib.hi_gemv_qkv_rope_w8(_p(x), x.stride(0), _p(normw), eps, _p(W), _p(scales), _p(bias), _p(out),
-                                    out.stride(0), x.shape[0], x.shape[1], Hq, Hkv, D, _p(cs), _p(pos), _p(kc), _p(vc),
-                                    kc.shape[2], _s())
-    else:
-        r = lib.hi_gemv_qkv_rope(_p(x), x.stride(0), _p(normw), eps, _p(W), _p(bias), _p(out), out.stride(0),
-                                 x.shape[0], x.shape[1], Hq, Hkv, D, _p(cs), _p(pos), _p(kc), _p(vc), kc.shape[2], _s())
-    _ok(r, "gemv_qkv_rope")
+    """The decode QKV projection with everything after it fused: RMSNorm(x) @ W^T (+ bias), RoPE on q
+    and k, q into out [M, Hq*D], k / v of row m into cache slot m at position pos[m]
+    (kc, vc: [slots, Hkv, max_seq, D]; cs: [max_seq, D/2, 2] cos/sin)."""
+    _need("gemv_qkv_rope", x, torch.float16, 2, rows=True)
+    q8 = _weight("gemv_qkv_rope", W, scales)
+    for t in (kc, vc):
+        _need("gemv_qkv_rope", t, torch.float16, 4)
+    _need("gemv_qkv_rope", pos, torch.int32, 1)
+    _need("gemv_qkv_rope", out, torch.float16, 2, rows=True)
+    _need("gemv_qkv_rope", bias, torch.float16, 1, optional=True)
+    M, K = x.shape
+    D, max_seq = kc.shape[3], kc.shape[2]
+    head = (ptr(x), x.stride(0), ptr(normw), eps, ptr(W))
+    tail = (ptr(bias), ptr(out), out.stride(0), M, K, Hq, Hkv, D, ptr(cs), ptr(pos), ptr(kc), ptr(vc), max_seq,
+            cur_stream())
+    rc = lib.hi_gemv_qkv_rope_w8(*head, ptr(scales), *tail) if q8 else lib.hi_gemv_qkv_rope(*head, *tail)
+    check_rc(rc, "gemv_qkv_rope")
     return out
 
 
 def gemm(A, W, out=None, epi=0, bias=None, scales=None):
-    """C (epi) A[M, K] @ W[N, K]^T on the MFMA GEMM (+ bias for epi 0)."""
+    """Prefill GEMM on the matrix cores: A [M, K] @ W^T with epilogue epi (0 store, + bias when given;
+    1 add into out; 2 SwiGLU over interleaved gate/up rows, out N/2 wide)."""
+    _need("gemm", A, torch.float16, 2, rows=True)
+    q8 = _weight("gemm", W, scales)
+    _need("gemm", bias, torch.float16, 1, optional=True)
     M, K = A.shape
     N = W.shape[0]
     if out is None:
-        out = torch.empty(M, N // 2 if epi == 2 else N, dtype=A.dtype, device=A.device)
-    _dev(A, W, out, bias, scales)
-    if _w8(W, scales):
-        r = lib.hi_gemm_w8(_p(A), A.stride(0), _p(W), _p(scales), _p(bias), _p(out), out.stride(0), M, N, K, epi, _s())
-    else:
-        r = lib.hi_gemm(_p(A), A.stride(0), _p(W), _p(bias), _p(out), out.stride(0), M, N, K, epi, _s())
-    _ok(r, "gemm")
+        out = _alloc_rows(A, M, N // 2 if epi == 2 else N)
+    _need("gemm", out, torch.float16, 2, rows=True)
+    head = (ptr(A), A.stride(0), ptr(W))
+    tail = (ptr(bias), ptr(out), out.stride(0), M, N, K, epi, cur_stream())
+    rc = lib.hi_gemm_w8(*head, ptr(scales), *tail) if q8 else lib.hi_gemm(*head, *tail)
+    check_rc(rc, "gemm")
     return out
 
 
+def _routing(xn, M, k):
+    return (torch.empty(M, k, dtype=torch.int32, device=xn.device),
+            torch.empty(M, k, dtype=torch.float32, device=xn.device))
+
+
+def _moe_work(xn, M, k, E, H, I):
+    return torch.empty(lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device=xn.device)
+
+
 def moe_router(xn, Wr, k, flags):
-    """Top-k experts of each normalised row xn [M, H] under router Wr [E, H]: (idx [M, k] int32,
-    weights [M, k] fp32), descending."""
+    """Routing of normalised rows xn [M, H] by router weights Wr [E, H]: the top k experts of each
+    row, best first, as (idx [M, k] int32, weights [M, k] fp32)."""
+    _need("moe_router", xn, torch.float16, 2, rows=True)
+    _need("moe_router", Wr, torch.float16, 2, rows=True)
     M, H = xn.shape
-    _dev(xn, Wr)
-    idx = torch.empty(M, k, dtype=torch.int32, device=xn.device)
-    w = torch.empty(M, k, dtype=torch.float32, device=xn.device)
-    _ok(lib.hi_moe_router(_p(xn), xn.stride(0), _p(Wr), M, Wr.shape[0], H, k, flags, _p(idx), _p(w), _s()), "moe_router")
+    idx, w = _routing(xn, M, k)
+    check_rc(lib.hi_moe_router(ptr(xn), xn.stride(0), ptr(Wr), M, Wr.shape[0], H, k, flags, ptr(idx), ptr(w),
+                               cur_stream()), "moe_router")
     return idx, w
 
 
 def moe_experts(xn, wgu, wdown, idx, w, x, flags, scale=1.0, path=0):
-    """x += MoE(xn) in place, given the routing: wgu [E, 2I, H] (gate/up interleaved per expert),
-    wdown [E, H, I]. path 0 auto, 1 GEMV, 2 grouped GEMM."""
+    """Adds the routed experts' SwiGLU MLPs to x in place: wgu [E, 2I, H] (gate/up interleaved by
+    16 rows), wdown [E, H, I]; path 0 chooses, 1 forces the GEMV kernels, 2 the grouped GEMM."""
+    for t in (xn, x):
+        _need("moe_experts", t, torch.float16, 2, rows=True)
+    for t in (wgu, wdown):
+        _need("moe_experts", t, torch.float16, 3)
     M, H = xn.shape
     E, I, k = wgu.shape[0], wdown.shape[2], idx.shape[1]
-    _dev(xn, wgu, wdown, idx, w, x)
-    work = torch.empty(lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device=xn.device)
-    _ok(lib.hi_moe_experts(_p(xn), xn.stride(0), _p(wgu), _p(wdown), _p(idx), _p(w), M, E, k, H, I, flags, scale, _p(x),
-                           x.stride(0), path, _p(work), _s()), "moe_experts")
+    work = _moe_work(xn, M, k, E, H, I)
+    check_rc(lib.hi_moe_experts(ptr(xn), xn.stride(0), ptr(wgu), ptr(wdown), ptr(idx), ptr(w), M, E, k, H, I, flags,
+                                scale, ptr(x), x.stride(0), path, ptr(work), cur_stream()), "moe_experts")
     return x
 
 
 def moe_route_experts(xn, Wr, wgu, wdown, k, x, flags, scale=1.0):
-    """Router and experts in one call: x += MoE(xn) in place with the routing computed on the way;
-    returns (idx [M, k] int32, weights [M, k] fp32) as moe_router would. The same bits as moe_router
-    then moe_experts(path=0); up to HIPINFER_GEMV_MAX rows the router runs inside the gate/up launch."""
+    """moe_router followed by moe_experts(path=0) as one library call with the same results; on the
+    GEMV path (up to HIPINFER_GEMV_MAX rows) the routing runs inside the gate/up launch. Returns the
+    routing (idx, weights)."""
+    for t in (xn, x):
+        _need("moe_route_experts", t, torch.float16, 2, rows=True)
     M, H = xn.shape
     E, I = wgu.shape[0], wdown.shape[2]
-    _dev(xn, Wr, wgu, wdown, x)
-    idx = torch.empty(M, k, dtype=torch.int32, device=xn.device)
-    w = torch.empty(M, k, dtype=torch.float32, device=xn.device)
-    work = torch.empty(lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device=xn.device)
-    _ok(lib.hi_moe_route_experts(_p(xn), xn.stride(0), _p(Wr), _p(wgu), _p(wdown), M, E, k, H, I, flags, scale, _p(x),
-                                 x.stride(0), _p(idx), _p(w), _p(work), _s()), "moe_route_experts")
+    idx, w = _routing(xn, M, k)
+    work = _moe_work(xn, M, k, E, H, I)
+    check_rc(lib.hi_moe_route_experts(ptr(xn), xn.stride(0), ptr(Wr), ptr(wgu), ptr(wdown), M, E, k, H, I, flags,
+                                      scale, ptr(x), x.stride(0), ptr(idx), ptr(w), ptr(work), cur_stream()),
+             "moe_route_experts")
     return idx, w
 
 
-# ------------------------------------------------------------------ int8 weight format (GPU)
 def decode_attn(q, kc, vc, pos, Hq, Hkv, out=None, work=None):
-    """Decode attention (reference scripts/hipinfer.py:180-190): q [B, ldq]; kc/vc [B, Hkv, max_seq, D]
-    fp16; pos [B] int32 (query b attends to keys 0..pos[b] of cache slot b). work: zeroed once,
-    hi_decode_work_bytes(B, Hq, Hkv, D) bytes (the kernel leaves its counters zeroed)."""
-    B = q.shape[0]
-    D = kc.shape[-1]
+    """One decode step of attention: sequence b's query q[b] [Hq*D] over the keys and values 0..pos[b]
+    of cache slot b (kc, vc: [B, Hkv, max_seq, D]). `work` (zeroed once, hi_decode_work_bytes) can be
+    reused across calls: the kernel leaves its counters at zero."""
+    _need("decode_attn", q, torch.float16, 2, rows=True)
+    for t in (kc, vc):
+        _need("decode_attn", t, torch.float16, 4)
+    _need("decode_attn", pos, torch.int32, 1)
+    B, D, max_seq = q.shape[0], kc.shape[3], kc.shape[2]
     if out is None:
-        out = torch.empty(B, Hq * D, dtype=torch.float16, device=q.device)
+        out = _alloc_rows(q, B, Hq * D)
     if work is None:
         work = torch.zeros(lib.hi_decode_work_bytes(B, Hq, Hkv, D), dtype=torch.uint8, device=q.device)
-    _dev(q, kc, vc, pos, out, work)
-    _ok(lib.hi_decode_attn(_p(q), q.stride(0), _p(kc), _p(vc), kc.shape[2], _p(pos), _p(out), out.stride(0), B, Hq, Hkv, D,
-                           _p(work), _s()), "decode_attn")
+    check_rc(lib.hi_decode_attn(ptr(q), q.stride(0), ptr(kc), ptr(vc), max_seq, ptr(pos), ptr(out), out.stride(0), B,
+                                Hq, Hkv, D, ptr(work), cur_stream()), "decode_attn")
     return out
 
 
 def rope_cache(qkv, Hq, Hkv, cs, kc, vc, pos=None, pos_base=0, slot_base=0):
-    """RoPE + KV-cache write after a QKV GEMM (reference scripts/hipinfer.py:164-168): qkv [M,
-    (Hq+2Hkv)*D] gets its q heads rotated in place; the rotated k and raw v rows go to kc/vc
-    [slots, Hkv, max_seq, D]; cs [max_seq, D/2, 2] fp16. Row m sits at pos[m] in slot
-    slot_base + m (decode), or at pos_base + m in slot slot_base (prefill)."""
-    D = kc.shape[-1]
-    _dev(qkv, cs, kc, vc, pos)
-    _ok(lib.hi_rope_cache(_p(qkv), qkv.stride(0), qkv.shape[0], Hq, Hkv, D, _p(cs), _p(pos), pos_base, slot_base,
-                          _p(kc), _p(vc), kc.shape[2], _s()), "rope_cache")
+    """After a QKV GEMM: rotates the q heads of qkv [M, (Hq+2Hkv)*D] in place and writes the rotated
+    k and the v of row m to the cache. Decode form (pos given): slot slot_base + m, position pos[m];
+    prefill form: slot slot_base, position pos_base + m."""
+    _need("rope_cache", qkv, torch.float16, 2, rows=True)
+    _need("rope_cache", pos, torch.int32, 1, optional=True)
+    D, max_seq = kc.shape[3], kc.shape[2]
+    check_rc(lib.hi_rope_cache(ptr(qkv), qkv.stride(0), qkv.shape[0], Hq, Hkv, D, ptr(cs), ptr(pos), pos_base,
+                               slot_base, ptr(kc), ptr(vc), max_seq, cur_stream()), "rope_cache")
 
 
-def flash_prefill(q, kc, vc, T, p0, Hq, Hkv, out=None):
-    """Causal prefill attention (reference scripts/hipinfer.py:171-177): q [T, ldq] with head h at
-    columns h*D, row t at position p0 + t; kc/vc [Hkv, max_seq, D] of one cache slot. Returns out
-    [T, Hq*D] fp16."""
-    D = kc.shape[-1]
+def _flash(q, kc, vc, T, p0, Hq, Hkv, out, lse):
+    _need("flash_prefill", q, torch.float16, 2, rows=True)
+    for t in (kc, vc):
+        _need("flash_prefill", t, torch.float16, 3)
+    D, max_seq = kc.shape[2], kc.shape[1]
     if out is None:
-        out = torch.empty(T, Hq * D, dtype=torch.float16, device=q.device)
-    _dev(q, kc, vc, out)
-    _ok(lib.hi_flash_prefill(_p(q), q.stride(0), _p(kc), _p(vc), kc.shape[1], _p(out), out.stride(0), T, p0, Hq, Hkv,
-                             D, _s()), "flash_prefill")
+        out = _alloc_rows(q, T, Hq * D)
+    args = (ptr(q), q.stride(0), ptr(kc), ptr(vc), max_seq, ptr(out), out.stride(0), T, p0, Hq, Hkv, D)
+    if lse is None:
+        check_rc(lib.hi_flash_prefill(*args, cur_stream()), "flash_prefill")
+    else:
+        check_rc(lib.hi_flash_prefill_lse(*args, ptr(lse), cur_stream()), "flash_prefill_lse")
     return out
 
 
+def flash_prefill(q, kc, vc, T, p0, Hq, Hkv, out=None):
+    """Causal attention for T prompt rows at positions p0.. of one cache slot: q [T, ldq] (head h at
+    columns h*D), kc / vc [Hkv, max_seq, D]; returns [T, Hq*D] fp16."""
+    return _flash(q, kc, vc, T, p0, Hq, Hkv, out, None)
+
+
 def flash_prefill_lse(q, kc, vc, T, p0, Hq, Hkv, out=None, lse=None):
-    """flash_prefill that also returns each row's log2-domain log-sum-exp, lse [Hq, T] fp32
-    (reference scripts/hipinfer.py:193-202)."""
-    D = kc.shape[-1]
-    if out is None:
-        out = torch.empty(T, Hq * D, dtype=torch.float16, device=q.device)
+    """flash_prefill, also returning every (head, row)'s log-sum-exp of its scaled logits in base 2,
+    lse [Hq, T] fp32: (out, lse)."""
     if lse is None:
         lse = torch.empty(Hq, T, dtype=torch.float32, device=q.device)
-    _dev(q, kc, vc, out, lse)
-    _ok(lib.hi_flash_prefill_lse(_p(q), q.stride(0), _p(kc), _p(vc), kc.shape[1], _p(out), out.stride(0), T, p0, Hq,
-                                 Hkv, D, _p(lse), _s()), "flash_prefill_lse")
-    return out, lse
+    _need("flash_prefill_lse", lse, torch.float32, 2)
+    return _flash(q, kc, vc, T, p0, Hq, Hkv, out, lse), lse
 
 
 def argmax(logits, out=None):
-    """Greedy token per row of logits [B, V] fp16 (reference hi_argmax, api.cu:838): NaN ranks
-    highest, ties go to the lowest index, an all -inf row gives 0."""
-    B, V = logits.shape
+    """Greedy token of each row of logits [B, V] (NaN beats every number, the lowest index wins a tie,
+    a row of -inf gives 0), as int32 [B]."""
     logits = logits.contiguous()
+    _need("argmax", logits, torch.float16, 2)
+    B, V = logits.shape
     if out is None:
         out = torch.empty(B, dtype=torch.int32, device=logits.device)
-    _dev(logits, out)
-    _ok(lib.hi_argmax(_p(logits), B, V, _p(out), _s()), "argmax")
+    check_rc(lib.hi_argmax(ptr(logits), B, V, ptr(out), cur_stream()), "argmax")
     return out
 
 
 def embed(tok, table, out=None):
-    """Embedding rows out[b] = table[tok[b]] (the reference engine's embed_kernel)."""
-    B = tok.shape[0]
+    """Embedding lookup: out[b] = table[tok[b]] for the int32 token ids tok [B]."""
+    _need("embed", tok, torch.int32, 1)
+    _need("embed", table, torch.float16, 2, rows=True)
     V, H = table.shape
     if out is None:
-        out = torch.empty(B, H, dtype=table.dtype, device=table.device)
-    _dev(tok, table, out)
-    _ok(lib.hi_embed(_p(tok), _p(table), V, H, _p(out), out.stride(0), B, _s()), "embed")
+        out = _alloc_rows(table, tok.shape[0], H)
+    check_rc(lib.hi_embed(ptr(tok), ptr(table), V, H, ptr(out), out.stride(0), tok.shape[0], cur_stream()), "embed")
     return out
 
 
+# ------------------------------------------------------------------ int8 weight format
 def quantize_rows(w):
-    """scripts/export.py:54-68 on the GPU, bit-exact: s[n] = fp16(max_k |w[n, k]| / 127),
-    q = clamp(round(w / s), -127, 127), q = 0 for an all-zero row. Returns (q int8, s fp16)."""
-    assert w.dtype == torch.float16 and w.dim() == 2
+    """Symmetric per-row int8 quantisation of fp16 weights w [N, K] on the GPU, bit for bit the
+    reference exporter's: scale s[n] = fp16(max |w[n]| / 127), q = round-half-even(w / s) clamped to
+    +-127 (an all-zero row gets q = 0). Returns (q int8 [N, K], s fp16 [N])."""
+    _need("quantize_rows", w, torch.float16, 2)
     w = w.contiguous()
-    _dev(w)
-    q = torch.empty(w.shape, dtype=torch.int8, device=w.device)
-    s = torch.empty(w.shape[0], dtype=torch.float16, device=w.device)
-    _ok(lib.hi_quantize_rows(_p(w), w.shape[0], w.shape[1], _p(q), _p(s), _s()), "quantize_rows")
+    N, K = w.shape
+    q = torch.empty(N, K, dtype=torch.int8, device=w.device)
+    s = torch.empty(N, dtype=torch.float16, device=w.device)
+    check_rc(lib.hi_quantize_rows(ptr(w), N, K, ptr(q), ptr(s), cur_stream()), "quantize_rows")
     return q, s
 
 
 def dequantize_rows(q, s):
-    """scripts/export.py:71-73: fp16(q * s), the weights the int8 GEMM computes with."""
+    """The fp16 weights int8 rows stand for, fp16(q * s): what the prefill GEMM multiplies by."""
+    _need("dequantize_rows", q, torch.int8, 2)
+    _need("dequantize_rows", s, torch.float16, 1)
     q = q.contiguous()
-    _dev(q, s)
     out = torch.empty(q.shape, dtype=torch.float16, device=q.device)
-    _ok(lib.hi_dequantize_rows(_p(q), _p(s), q.shape[0], q.shape[1], _p(out), _s()), "dequantize_rows")
+    check_rc(lib.hi_dequantize_rows(ptr(q), ptr(s), q.shape[0], q.shape[1], ptr(out), cur_stream()), "dequantize_rows")
     return out
 
 
 def interleave_gate_up(gate, up, group=16):
-    """scripts/export.py:97-101: [2I, H] with 16 gate rows, then the same 16 up rows, per group."""
-    inter, hidden = gate.shape
-    g = gate.reshape(inter // group, group, hidden)
-    u = up.reshape(inter // group, group, hidden)
-    return torch.stack([g, u], dim=1).reshape(2 * inter, hidden)
+    """The fused gate/up layout: for every block of `group` intermediate units, their gate rows
+    followed by their up rows, [2I, H] from gate [I, H] and up [I, H] (any device or dtype)."""
+    inter = gate.shape[0]
+    if up.shape != gate.shape or inter % group:
+        raise ValueError("hipinfer_amd.interleave_gate_up: gate and up must match, rows a multiple of the group")
+    unit = torch.arange(inter, device=gate.device)
+    # destination row of gate unit u: its group's first row, plus its place in the group
+    dest = (unit // group) * (2 * group) + unit % group
+    fused = gate.new_empty((2 * inter,) + tuple(gate.shape[1:]))
+    fused[dest] = gate
+    fused[dest + group] = up
+    return fused
+
+
+# ------------------------------------------------------------------ engine
+def _ints(values):
+    values = list(values)
+    return (ctypes.c_int * max(1, len(values)))(*values), len(values)
 
 
 class Engine:
-    """The reference's Engine (scripts/hipinfer.py:334-500) over this library's engine entry
-    points, one GPU: a weight file in the export format (versions 2, 3, 4) loaded for max_batch
-    slots of max_seq positions, greedy prefill / decode, per-slot token history. tp must be 1.
-    Bad arguments raise ValueError (the reason is printed on stderr)."""
+    """A model from a weight file (the reference exporter's format: version 2 dense, 3 MoE, 4 int8)
+    served on one GPU: max_batch cache slots of max_seq positions each, prompts prefilled in chunks
+    of max_prefill rows, greedy decoding with the per-slot token history kept on the device.
+
+    The reference's Engine API: prefill, prefill_logits, decode, history, logits, set_state, rewind,
+    verify, generate, close, plus the model's shape as attributes. tp must be 1 (one GPU per engine;
+    `devices`, if given, names it). A call the library rejects raises ValueError, with the reason on
+    stderr."""
+
+    MAX_VERIFY = lib.hi_verify_max_rows()  # draft rows per verify() call (k + 1 for k draft tokens)
+    _CONFIG = ("vocab", "hidden", "inter", "layers", "heads", "kv_heads", "head_dim", "max_pos", "tied", "qkv_bias",
+               "window")
 
     def __init__(self, path, max_batch=8, max_seq=2048, max_prefill=1024, tp=1, devices=None):
         if tp != 1:
-            raise ValueError("hipinfer_amd.Engine: one GPU per engine (tp=1)")
-        dev = torch.cuda.current_device() if devices is None else list(devices)[0]
-        self.tp = 1
-        self.device = torch.device("cuda", dev)
-        self.h = lib.hi_load_tp(os.fsencode(path), max_batch, max_seq, max_prefill, 1, (C.c_int * 1)(dev))
+            raise ValueError("hipinfer_amd.Engine: this build serves a model on one GPU (tp=1)")
+        gpu = torch.cuda.current_device() if devices is None else int(list(devices)[0])
+        self.tp, self.device = 1, torch.device("cuda", gpu)
+        self.max_batch, self.max_seq, self.max_prefill = max_batch, max_seq, max_prefill
+        devs, _ = _ints([gpu])
+        self.h = lib.hi_load_tp(os.fsencode(path), max_batch, max_seq, max_prefill, 1, devs)
         if not self.h:
-            raise RuntimeError("hi_load failed")
-        cfg = (C.c_int * 11)()
-        lib.hi_config(self.h, cfg)
-        (self.vocab, self.hidden, self.inter, self.layers, self.heads, self.kv_heads, self.head_dim, self.max_pos,
-         tied, qkv_bias, self.window) = list(cfg)
-        self.tied, self.qkv_bias = bool(tied), bool(qkv_bias)
-        moe = (C.c_int * 3)()
+            raise RuntimeError(f"hipinfer_amd.Engine: loading {path} failed (reason on stderr)")
+        fields = (ctypes.c_int * len(self._CONFIG))()
+        lib.hi_config(self.h, fields)
+        for name, value in zip(self._CONFIG, fields):
+            setattr(self, name, bool(value) if name in ("tied", "qkv_bias") else value)
+        moe = (ctypes.c_int * 3)()
         lib.hi_moe_config(self.h, moe)
-        self.n_experts, self.top_k, self.moe_flags = list(moe)
-        self.quant = lib.hi_weight_quant(self.h)
-        self.max_seq, self.max_batch, self.max_prefill = max_seq, max_batch, max_prefill
+        self.n_experts, self.top_k, self.moe_flags = moe  # zeros for a dense model
+        self.quant = lib.hi_weight_quant(self.h)  # 0 fp16 projections, 1 int8 with fp16 row scales
         self.weight_bytes = lib.hi_weight_bytes(self.h)
-        self.kv_bytes_per_token = 2 * self.layers * self.kv_heads * self.head_dim * 2
+        row = self.kv_heads * self.head_dim * 2  # one position's k (or v) in one layer, fp16
+        self.kv_bytes_per_token = 2 * row * self.layers
 
-    @staticmethod
-    def _ok(r, what):
-        if r < 0:
-            raise ValueError(f"hipinfer_amd {what}: bad arguments (see stderr)")
-        return r
+    def _run(self, rc, what):
+        if rc < 0:
+            raise ValueError(f"hipinfer_amd.Engine.{what}: the library rejected the call (reason on stderr)")
+        return rc
 
     def prefill(self, slot, tokens, p0=0):
-        arr = (C.c_int * len(tokens))(*tokens)
-        return self._ok(lib.hi_prefill(self.h, slot, arr, len(tokens), p0), "prefill")
+        """Runs `tokens` through the model into cache slot `slot` at positions p0..; returns the greedy
+        next token, which the slot will feed to its next decode step."""
+        arr, n = _ints(tokens)
+        return self._run(lib.hi_prefill(self.h, slot, arr, n, p0), "prefill")
 
     def prefill_logits(self, slot, tokens, p0=0):
-        """Prefill and return the fp16 logits of every position, [T, vocab] on the GPU."""
-        arr = (C.c_int * len(tokens))(*tokens)
-        out = torch.empty(len(tokens), self.vocab, dtype=torch.float16, device=self.device)
-        self._ok(lib.hi_prefill_logits(self.h, slot, arr, len(tokens), p0, C.c_void_p(out.data_ptr())),
-                 "prefill_logits")
-        return out
+        """prefill, returning the fp16 logits of every prompt position, [len(tokens), vocab] on the GPU."""
+        arr, n = _ints(tokens)
+        logits = torch.empty(n, self.vocab, dtype=torch.float16, device=self.device)
+        self._run(lib.hi_prefill_logits(self.h, slot, arr, n, p0, ptr(logits)), "prefill_logits")
+        return logits
 
     def decode(self, B, steps, graph=True):
-        return self._ok(lib.hi_decode(self.h, B, steps, int(graph)), "decode")
+        """`steps` greedy decode steps of slots 0..B-1 (replayed as a captured graph unless graph is
+        False); returns the library's timing figure for the run."""
+        return self._run(lib.hi_decode(self.h, B, steps, int(graph)), "decode")
 
     def history(self, slot, start, n):
-        arr = (C.c_int * n)()
-        self._ok(lib.hi_history(self.h, slot, start, n, arr), "history")
-        return list(arr)
+        """Tokens at positions start .. start + n - 1 of a slot's history, as a list."""
+        arr, _ = _ints([0] * n)
+        self._run(lib.hi_history(self.h, slot, start, n, arr), "history")
+        return list(arr)[:n]
 
     def logits(self, B):
+        """The last decode step's logits of slots 0..B-1, [B, vocab] fp16 on the GPU."""
         out = torch.empty(B, self.vocab, dtype=torch.float16, device=self.device)
-        self._ok(lib.hi_logits(self.h, B, C.c_void_p(out.data_ptr())), "logits")
+        self._run(lib.hi_logits(self.h, B, ptr(out)), "logits")
         return out
 
     def set_state(self, tokens, positions):
-        """Next input token and its position for slots [0, len(tokens))."""
-        B = len(tokens)
-        assert len(positions) == B
-        self._ok(lib.hi_set_state(self.h, B, (C.c_int * B)(*tokens), (C.c_int * B)(*positions)), "set_state")
+        """Sets slot i's next input token to tokens[i], fed at position positions[i]."""
+        if len(tokens) != len(positions):
+            raise ValueError("hipinfer_amd.Engine.set_state: one position per token")
+        tok, B = _ints(tokens)
+        pos, _ = _ints(positions)
+        self._run(lib.hi_set_state(self.h, B, tok, pos), "set_state")
 
     def rewind(self, slot, length, next_token):
-        """Cut slot's cache to `length` positions; the next decode step feeds next_token there."""
-        self._ok(lib.hi_rewind(self.h, slot, length, next_token), "rewind")
-
-    MAX_VERIFY = lib.hi_verify_max_rows() if hasattr(lib, "hi_verify_max_rows") else 0
+        """Truncates a slot to its first `length` cached positions; its next decode step feeds
+        next_token at position `length`."""
+        self._run(lib.hi_rewind(self.h, slot, length, next_token), "rewind")
 
     def verify(self, slot, tokens, p0, graph=True, logits=False):
-        """Greedy next token after each of `tokens`, fed at positions p0.. of `slot` (whose cache
-        must hold positions < p0), computed by the batch-of-one decode kernels, so entry i is
-        exactly the token plain greedy decoding produces at p0 + i given the same prefix. Writes
-        the rows' k/v; leaves the slot's next token and position alone (see rewind). With
-        logits=True also returns the [len(tokens), vocab] fp16 logits. Dense models."""
-        R = len(tokens)
-        out = (C.c_int * R)()
+        """Speculative verification of up to MAX_VERIFY rows: tokens[i] is fed at position p0 + i of
+        `slot` (whose cache must already hold the positions before p0), all rows in one pass through
+        the batch-of-one decode kernels, so entry i of the result is the token plain greedy decoding
+        would emit after the same prefix, bit for bit. The rows' k / v stay in the cache; the slot's
+        next token and position are not changed (rewind sets them after acceptance). Dense models.
+        Returns the list of tokens, or (tokens, logits [R, vocab] fp16 on the GPU) with logits=True."""
+        arr, R = _ints(tokens)
+        picked = (ctypes.c_int * max(1, R))()
         lg = torch.empty(R, self.vocab, dtype=torch.float16, device=self.device) if logits else None
-        self._ok(lib.hi_verify(self.h, slot, (C.c_int * R)(*tokens), R, p0, out,
-                               None if lg is None else C.c_void_p(lg.data_ptr()), int(graph)), "verify")
-        return (list(out), lg) if logits else list(out)
+        self._run(lib.hi_verify(self.h, slot, arr, R, p0, picked, ptr(lg), int(graph)), "verify")
+        toks = list(picked)[:R]
+        return (toks, lg) if logits else toks
 
     def generate(self, prompt, n_new, graph=True):
-        """Greedy: returns n_new tokens (the first comes from prefill)."""
-        first = self.prefill(0, prompt)
+        """Greedy continuation of `prompt` in slot 0: n_new token ids, the prefill's prediction first."""
+        if n_new < 1:
+            return []
+        tokens = [self.prefill(0, prompt)]
         if n_new > 1:
             self.decode(1, n_new - 1, graph)
-        return [first] + self.history(0, len(prompt) + 1, n_new - 1)
+            tokens += self.history(0, len(prompt) + 1, n_new - 1)
+        return tokens
 
     def close(self):
-        if self.h:
-            lib.hi_free(self.h)
-            self.h = None
+        """Frees the engine's GPU memory (idempotent)."""
+        handle, self.h = getattr(self, "h", None), None
+        if handle:
+            lib.hi_free(handle)
 
     def __del__(self):
         try:

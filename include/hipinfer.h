@@ -65,6 +65,10 @@ int hi_gemm_force_config(int cfg);
 int hi_gemm_force_splits(int splits);
 int hi_gemm_num_configs(void);
 int hi_gemm_config_desc(int cfg, char* out, int n);
+/* Test hook, no counterpart in the reference: the (tile config, split count) the calling thread's
+ * last hi_gemm / hi_gemm_w8 launch ran with, so a test can tell a forced config that ran from one
+ * that did not fit the shape or weight format and fell back to the automatic choice. */
+int hi_gemm_last_choice(int* cfg, int* splits);
 
 /* ---- mixture of experts (fp16 experts, E <= 256, k <= 16)
  * Router + top-k of M normalised rows xn[M, H] under Wr[E, H]: idx[M, k] int, w[M, k] fp32, descending;

@@ -38,10 +38,51 @@ def test_library_holds_gfx950_code_objects():
     assert b"gfx950" in blob
 
 
-def test_host_mirror_imports_and_binds(monkeypatch):
+def header_prototypes():
+    """{name: (return kind, [argument kinds])} from include/hipinfer.h, in the Python module's kinds:
+    pointers are ptr, except char pointers (strings) str; long long i64; size_t size."""
+    src = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "hipinfer.h")).read(), flags=re.S)
+
+    def kind(decl):
+        decl = decl.replace("const ", "").strip()
+        if "char*" in decl.replace(" ", ""):
+            return "str"
+        if "*" in decl:
+            return "ptr"
+        t = decl.split()[0]
+        return {"long": "i64", "size_t": "size", "int": "int", "float": "float", "void": "void"}[t]
+
+    out = {}
+    for m in re.finditer(r"(?m)^([A-Za-z_][\w* ]*?)\s*\b(hi_\w+)\s*\(([^)]*)\)\s*;", src):
+        args = [a for a in m.group(3).split(",") if a.strip() and a.strip() != "void"]
+        out[m.group(2)] = (kind(m.group(1)), [kind(a) for a in args])
+    return out
+
+
+def test_host_mirror_binds_the_header_prototypes():
+    """The Python module's prototype table (its ctypes argtypes / restype) is the header's, symbol
+    for symbol and argument for argument."""
     from hipinfer_amd import hipinfer
-    for name in ["hi_gemv", "hi_gemv_w8", "hi_gemv_qkv_rope", "hi_gemv_qkv_rope_w8", "hi_rmsnorm"]:
+    hdr = header_prototypes()
+    assert set(hipinfer.SIGNATURES) == set(hdr)
+    for name, sig in hdr.items():
+        assert hipinfer.SIGNATURES[name] == sig, name
         assert getattr(hipinfer.lib, name).argtypes is not None
+
+
+def test_interleave_gate_up_layout():
+    """Rows 32j .. 32j+15 are gate rows 16j .., rows 32j+16 .. 32j+31 the same up rows (the reference
+    exporter's layout, export.py:97-101), on the CPU (no GPU needed)."""
+    import torch
+    from hipinfer_amd import hipinfer
+    I, H = 48, 3
+    g = torch.arange(I * H, dtype=torch.float32).reshape(I, H)
+    u = -g - 1
+    f = hipinfer.interleave_gate_up(g, u)
+    for r in range(2 * I):
+        grp, i = divmod(r, 32)
+        src = g if i < 16 else u
+        assert torch.equal(f[r], src[grp * 16 + i % 16])
 
 
 def test_product_path_never_loads_the_oracle():

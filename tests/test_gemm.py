@@ -58,13 +58,64 @@ def gemm_check(hi, O, name, A, W, r, epi=0, bias=None, scales=None, res=None, to
     torch.cuda.synchronize()
 
 
-# every tile configuration (the automatic choice is -1); configs past the library's count skip
-CFGS = [-1] + list(range(17))
+def _num_configs():
+    """The library's tile-config count (a constant; reading it needs no GPU)."""
+    import ctypes
+    import os
+    so = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "hipinfer_amd", "libhipinfer.so")
+    try:
+        return ctypes.CDLL(so).hi_gemm_num_configs()
+    except OSError:
+        return 19
+
+
+NUM_CFGS = _num_configs()
+# every tile configuration, and the automatic choice (-1)
+CFGS = list(range(-1, NUM_CFGS))
 
 
 def need_cfg(hi, cfg):
     if cfg >= hi.lib.hi_gemm_num_configs():
         pytest.skip(f"the library has {hi.lib.hi_gemm_num_configs()} configs")
+
+
+def last_choice(hi):
+    import ctypes
+    c, sp = ctypes.c_int(), ctypes.c_int()
+    hi.lib.hi_gemm_last_choice(ctypes.byref(c), ctypes.byref(sp))
+    return c.value, sp.value
+
+
+def cfg_shape(hi, cfg):
+    """(bm, bn, bk, waves) of a tile config, from hi_gemm_config_desc."""
+    import ctypes
+    import re
+    buf = ctypes.create_string_buffer(128)
+    hi.lib.hi_gemm_config_desc(cfg, buf, 128)
+    m = re.search(r"(\d+)x(\d+)x(\d+) waves (\d+)x(\d+)", buf.value.decode())
+    return int(m[1]), int(m[2]), int(m[3]), int(m[4]) * int(m[5])
+
+
+def cfg_runs(hi, cfg, q8, K):
+    """Whether a forced config runs for this weight format and K, by the library's documented rule:
+    every wave issues whole 1 KB DMA instructions per K tile for the A tile and the W tile (int8 W rows
+    are half as wide), and the 128-deep tiles take fp16 weights with K % 128 == 0; otherwise the
+    automatic choice runs instead."""
+    bm, bn, bk, nw = cfg_shape(hi, cfg)
+    a, b = bm * 2 * bk, bn * (bk if q8 else 2 * bk)
+    ok = a % (1024 * nw) == 0 and b % (1024 * nw) == 0 and a >= 1024 * nw and b >= 1024 * nw
+    return ok and (bk < 128 or (not q8 and K % 128 == 0))
+
+
+def assert_ran(hi, cfg, q8, K, what):
+    """The last launch ran the forced config when it can run, and something else when it cannot."""
+    if cfg < 0:
+        return
+    got = last_choice(hi)[0]
+    if cfg_runs(hi, cfg, q8, K):
+        assert got == cfg, f"{what}: forced config {cfg} did not run (ran {got})"
+    else:
+        assert got != cfg, f"{what}: config {cfg} ran where it does not fit"
 
 
 SHAPES = [(128, 2560, 2048), (77, 2048, 5632), (512, 32000, 2048), (1000, 2048, 2048), (300, 1152, 896),
@@ -81,6 +132,7 @@ def test_gemm_configs(hi, O, cfg):
             A = h16(r, M, K)
             W = h16(r, N, K, sd=0.02)
             gemm_check(hi, O, f"gemm cfg={cfg} M={M} N={N} K={K}", A, W, r)
+            assert_ran(hi, cfg, False, K, f"M={M} N={N} K={K}")
         M, H, I = 200, 2048, 5632
         A = h16(r, M, H)
         W = h16(r, 1152, H, sd=0.02)
@@ -92,6 +144,7 @@ def test_gemm_configs(hi, O, cfg):
         a = h16(r, M, I)
         W2 = h16(r, H, I, sd=0.02)
         gemm_check(hi, O, f"gemm+residual cfg={cfg}", a, W2, r, epi=1, res=res, tol=(4e-3, 2e-3))
+        assert_ran(hi, cfg, False, I, "residual")
         # SwiGLU with a partial last column tile: nothing may be written past column I2
         I2 = 608
         gu2 = interleave(h16(r, I2, H, sd=0.02), h16(r, I2, H, sd=0.02))
@@ -115,7 +168,7 @@ def test_gemm_writes_nothing_past_n(hi, O, cfg):
     hi.lib.hi_gemm_force_config(cfg)
     try:
         for M, N, K, epi, sp in [(5, 1552, 992, 0, 1), (70, 1040, 1024, 1, 1), (33, 1552, 1024, 0, 4),
-                                 (5, 528, 2048, 1, 4)]:
+                                 (5, 528, 2048, 1, 4), (130, 1040, 1536, 0, 1), (40, 528, 1024, 1, 3)]:
             hi.lib.hi_gemm_force_splits(sp)
             A = h16(r, M, K)
             W = h16(r, N, K, sd=0.02)
@@ -129,6 +182,7 @@ def test_gemm_writes_nothing_past_n(hi, O, cfg):
             got = host(bd)
             ref = O.gemm(A, W, epi=epi, bias=b, out=res.copy() if epi == 1 else None)
             check(f"cfg={cfg} M={M} N={N} epi={epi} split={sp}", got[:M, :N], ref, 4e-3, 3e-3)
+            assert_ran(hi, cfg, False, K, f"M={M} N={N} K={K}")
             assert (got[:, N:] == 7.0).all() and (got[M] == 7.0).all(), f"cfg={cfg} N={N}: wrote past column N or row M"
     finally:
         hi.lib.hi_gemm_force_config(-1)
@@ -171,14 +225,15 @@ def test_gemm_short_k(hi, O):
     tiles leaves no empty split."""
     r = rng(330)
     try:
-        for cfg in [-1, 0, 1, 5, 6, 10, 12, 13, 14, 15]:
+        for cfg in CFGS:
             hi.lib.hi_gemm_force_config(cfg)
             for sp in [1, 2]:
                 hi.lib.hi_gemm_force_splits(sp)
-                for M, K in [(300, 32 * sp), (300, 64 * sp), (129, 96), (33, 32)]:
+                for M, K in [(300, 32 * sp), (300, 64 * sp), (129, 96), (33, 32), (300, 128 * sp), (70, 384)]:
                     x = h16(r, M, K)
                     W = h16(r, 1024, K, sd=0.02)
                     gemm_check(hi, O, f"short-K cfg={cfg} split={sp} M={M} K={K}", x, W, r)
+                    assert_ran(hi, cfg, False, K, f"short-K split={sp} M={M} K={K}")
     finally:
         hi.lib.hi_gemm_force_config(-1)
         hi.lib.hi_gemm_force_splits(-1)
@@ -195,6 +250,7 @@ def test_gemm_int8(hi, O, cfg):
             q, s = O.quantize_rows(h16(r, N, K, sd=0.02))
             A = h16(r, M, K)
             gemm_check(hi, O, f"int8 cfg={cfg} M={M} N={N} K={K}", A, q, r, scales=s)
+            assert_ran(hi, cfg, True, K, f"int8 M={M} N={N} K={K}")
         M = 200
         A = h16(r, M, H)
         q, s = O.quantize_rows(h16(r, 2560, H, sd=0.02))
@@ -354,3 +410,70 @@ def test_gemm_rejects_bad_shapes(hi):
     W = torch.zeros(48, 64, dtype=torch.float16, device="cuda")
     with pytest.raises(ValueError):
         hi.gemm(A, W, epi=2)  # SwiGLU needs N % 32 == 0
+
+
+# the 128-deep tiles and their 64-deep twins: (deep, twin)
+DEEP_TWINS = [(17, 3), (18, 7)]
+
+
+@pytest.mark.parametrize("deep,twin", DEEP_TWINS)
+def test_gemm_deep_k_tiles_bit_identical(hi, O, deep, twin):
+    """A 128-deep K tile sums its k range in the order of two consecutive 64-deep tiles, so at one
+    split the 128-deep config gives the bits of its 64-deep twin (same BM x BN and waves), for every
+    epilogue. With 3 splits the split boundaries differ (K tiles of 128 against 64), so there the
+    sums are only checked against the oracle."""
+    need_cfg(hi, deep)
+    assert cfg_shape(hi, deep)[:2] == cfg_shape(hi, twin)[:2] and cfg_shape(hi, deep)[2] == 128
+    r = rng(380 + deep)
+    H, I = 3072, 8192
+    cases = [("store", h16(r, 128, H), h16(r, 5120, H, sd=0.02), 0, h16(r, 5120), None),
+             ("residual", h16(r, 100, I), h16(r, H, I, sd=0.02), 1, None, h16(r, 100, H)),
+             ("swiglu", h16(r, 77, H), interleave(h16(r, 1024, H, sd=0.02), h16(r, 1024, H, sd=0.02)), 2, None, None),
+             ("store K=1152", h16(r, 33, 1152), h16(r, 2048, 1152, sd=0.02), 0, None, None)]
+    try:
+        for name, A, W, epi, bias, res in cases:
+            outs = []
+            for c in (deep, twin):
+                hi.lib.hi_gemm_force_config(c)
+                hi.lib.hi_gemm_force_splits(1)
+                o = cuda(res) if res is not None else None
+                outs.append(host(hi.gemm(cuda(A), cuda(W), out=o, epi=epi, bias=None if bias is None else cuda(bias))))
+                assert last_choice(hi) == (c, 1), f"{name}: config {c} split 1 did not run"
+            assert np.array_equal(bits(outs[0]), bits(outs[1])), f"{name}: config {deep} differs from {twin}"
+            ref = O.gemm(A, W, epi=epi, bias=bias, out=None if res is None else res.copy())
+            check(f"deep cfg={deep} {name}", outs[0], ref, 4e-3, 3e-3)
+        # three splits over K = 2048 (16 deep tiles -> 6 + 6 + 4; the twin would split 32 tiles 11 + 11 + 10)
+        hi.lib.hi_gemm_force_config(deep)
+        hi.lib.hi_gemm_force_splits(3)
+        for M, N, epi in [(64, 2560, 0), (128, 3072, 1), (40, 4096, 2)]:
+            A = h16(r, M, 2048)
+            W = h16(r, N, 2048, sd=0.02) if epi != 2 else interleave(h16(r, N // 2, 2048, sd=0.02),
+                                                                     h16(r, N // 2, 2048, sd=0.02))
+            res = h16(r, M, N) if epi == 1 else None
+            gemm_check(hi, O, f"deep cfg={deep} split=3 M={M} N={N} epi={epi}", A, W, r, epi=epi, res=res,
+                       tol=(4e-3, 4e-3) if epi == 2 else (4e-3, 2e-3))
+            assert last_choice(hi) == (deep, 3), f"config {deep} split 3 did not run"
+    finally:
+        hi.lib.hi_gemm_force_config(-1)
+        hi.lib.hi_gemm_force_splits(-1)
+
+
+@pytest.mark.parametrize("M", [128, 512, 1024])
+@pytest.mark.parametrize("q8", [False, True], ids=["fp16", "int8"])
+def test_gemm_llama32_3b_layer(hi, O, M, q8):
+    """C3 (Llama-3.2-3B prefill) at the benchmarked M with the automatic (tuned) choice: QKV
+    3072 -> 5120 (store), o 3072 -> 3072 (+ residual), gate/up 3072 -> 2 x 8192 (SwiGLU), down
+    8192 -> 3072 (+ residual), fp16 and int8 weights; sampled rows against the oracle."""
+    r = rng(400 + M + q8)
+    H, I, QKV = 3072, 8192, 5120
+    for name, N, K, epi in [("qkv", QKV, H, 0), ("o", H, H, 1), ("gate/up", 2 * I, H, 2), ("down", H, I, 1)]:
+        A = h16(r, M, K)
+        W = h16(r, N, K, sd=0.02) if epi != 2 else interleave(h16(r, I, H, sd=0.02), h16(r, I, H, sd=0.02))
+        s = None
+        if q8:
+            W, s = O.quantize_rows(W)
+        res = h16(r, M, N) if epi == 1 else None
+        tol = (4e-3, 4e-3) if epi == 2 else (4e-3, 2e-3) if epi == 1 else (3e-3, 3e-3)
+        gemm_check(hi, O, f"C3 {name} {'int8' if q8 else 'fp16'} M={M}", A, W, r, epi=epi, scales=s, res=res, tol=tol)
+        c, sp = last_choice(hi)
+        assert 0 <= c < NUM_CFGS and sp >= 1, (name, c, sp)

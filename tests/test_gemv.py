@@ -142,7 +142,10 @@ def test_row_independence(hi, O, q, norm):
             assert np.array_equal(bits(got[m]), bits(ones[m])), f"M={M} row {m}"
 
 
-QKV = [(64, 32, 4, 2048, False), (128, 24, 8, 3072, False), (128, 12, 2, 1536, True), (64, 14, 2, 896, True)]
+# (D, Hq, Hkv, K, bias): TinyLlama, Llama-3.2-3B, Qwen2.5-1.5B (C4, with bias), a 14-head shape,
+# and Llama-3.1-8B (C2: 32 q heads, 8 kv heads, head_dim 128, K = 4096)
+QKV = [(64, 32, 4, 2048, False), (128, 24, 8, 3072, False), (128, 12, 2, 1536, True), (64, 14, 2, 896, True),
+       (128, 32, 8, 4096, False)]
 
 
 def rope_table(S, D, theta=10000.0):
@@ -315,3 +318,100 @@ def test_grouped_units_lm_head_sized(hi, O, q):
         assert np.array_equal(bits(got[m]), bits(ones[m])), f"residual row {m}"
     ref = O.gemv(x[:8], Wh, out=res[:, cols].copy(), epi=1, scales=sh)
     check(f"grouped {'int8' if q else 'fp16'} residual sampled", got[:, cols], ref, 4e-3, 2e-3)
+
+
+def gpu_weights(hi, seed, N, K, q):
+    """[N, K] weights ~N(0, 0.02) generated on the GPU (lm_head-sized matrices), int8-quantised on the
+    GPU when q (the quantiser is bit-exact against the oracle, test_quantize_rows_bit_exact)."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    W = (torch.randn(N, K, generator=g, device="cuda") * 0.02).half()
+    return (W, None) if not q else hi.quantize_rows(W)
+
+
+def sampled_lm_head(hi, O, r, Wd, sd, x, nw, name):
+    """Fused-norm lm_head GEMV at full size; 248 sampled columns plus the last 8 against the oracle
+    (columns are independent, so the oracle's GEMV over the sampled rows is exact for them)."""
+    import torch
+    N = Wd.shape[0]
+    got = host(hi.gemv(cuda(x), Wd, normw=cuda(nw), scales=sd))
+    cols = np.concatenate([np.sort(r.choice(N - 8, 248, replace=False)), np.arange(N - 8, N)])
+    idx = torch.from_numpy(cols).cuda()
+    ref = O.gemv(x, host(Wd[idx]), normw=nw, scales=None if sd is None else host(sd[idx]))
+    check(name, got[:, cols], ref, 3e-3, 3e-3)
+
+
+@pytest.mark.parametrize("q", [False, True], ids=["fp16", "int8"])
+def test_llama31_8b_lm_head(hi, O, q):
+    """C2's lm_head, 4096 -> 128256 with the final RMSNorm fused, at 1 and 8 rows."""
+    r = rng(30 + q)
+    H = 4096
+    Wd, sd = gpu_weights(hi, 30, 128256, H, q)
+    nw = (r.random(H) + 0.5).astype(np.float16)
+    for M in [1, 8]:
+        sampled_lm_head(hi, O, r, Wd, sd, h16(r, M, H), nw, f"C2 lm_head {'int8' if q else 'fp16'} M={M}")
+
+
+@pytest.mark.parametrize("q", [False, True], ids=["fp16", "int8"])
+def test_qwen25_1p5b_shapes(hi, O, q):
+    """C4 (Qwen2.5-1.5B) at the batch / verify widths N = 1, 2, 5, 8: fused-norm gate/up + SwiGLU
+    1536 -> 2 x 8960, down + residual 8960 -> 1536, fused-norm QKV + bias + RoPE 1536 -> 2048 (12 q
+    heads, 2 kv heads, head_dim 128), all checked whole against the oracle, and the 151936-row
+    lm_head on sampled columns."""
+    r = rng(40 + q)
+    H, I, D, Hq, Hkv, S = 1536, 8960, 128, 12, 2, 256
+    gu = interleave(h16(r, I, H, sd=0.02), h16(r, I, H, sd=0.02))
+    dn = h16(r, H, I, sd=0.02)
+    wq = h16(r, (Hq + 2 * Hkv) * D, H, sd=0.02)
+    bq = h16(r, (Hq + 2 * Hkv) * D)
+    sg = sdn = sq = None
+    if q:
+        gu, sg = q8(O, gu)
+        dn, sdn = q8(O, dn)
+        wq, sq = q8(O, wq)
+    gud, dnd, wqd = cuda(gu), cuda(dn), cuda(wq)
+    sgd, sdnd, sqd = (None, None, None) if not q else (cuda(sg), cuda(sdn), cuda(sq))
+    cs = rope_table(S, D)
+    nw = (r.random(H) + 0.5).astype(np.float16)
+    Wl, sl = gpu_weights(hi, 41, 151936, H, q)
+    kind = "int8" if q else "fp16"
+    for M in [1, 2, 5, 8]:
+        x = h16(r, M, H)
+        got = host(hi.gemv(cuda(x), gud, epi=2, normw=cuda(nw), scales=sgd))
+        check(f"C4 gate/up {kind} N={M}", got, O.gemv(x, gu, epi=2, normw=nw, scales=sg), 3e-3, 3e-3)
+        a = h16(r, M, I)
+        res = h16(r, M, H)
+        out = cuda(res)
+        hi.gemv(cuda(a), dnd, out=out, epi=1, scales=sdnd)
+        check(f"C4 down {kind} N={M}", host(out), O.gemv(a, dn, out=res.copy(), epi=1, scales=sdn), 4e-3, 2e-3)
+        pos = r.integers(0, S, M).astype(np.int32)
+        out_r = np.zeros((M, Hq * D), np.float16)
+        kc_r = np.zeros((M, Hkv, S, D), np.float16)
+        vc_r = np.zeros_like(kc_r)
+        O.gemv_qkv_rope(x, wq, nw, Hq, Hkv, cs, pos, kc_r, vc_r, out_r, bias=bq, scales=sq)
+        out = cuda(np.zeros((M, Hq * D), np.float16))
+        kc, vc = cuda(np.zeros_like(kc_r)), cuda(np.zeros_like(vc_r))
+        hi.gemv_qkv_rope(cuda(x), wqd, cuda(nw), Hq, Hkv, cuda(cs), cuda(pos), kc, vc, out, bias=cuda(bq), scales=sqd)
+        check(f"C4 qkv+rope {kind} N={M}: q", host(out), out_r, 2e-2, 2e-3)
+        check(f"C4 qkv+rope {kind} N={M}: k cache", host(kc), kc_r, 2e-2, 2e-3)
+        check(f"C4 qkv+rope {kind} N={M}: v cache", host(vc), vc_r, 2e-2, 2e-3)
+        sampled_lm_head(hi, O, r, Wl, sl, x, nw, f"C4 lm_head {kind} N={M}")
+
+
+def test_int8_positive_activations_with_outliers(hi, O):
+    """int8 weights against all-positive activations with outliers at long K (SwiGLU-like down
+    projection inputs, K = 14336, |x| up to 100): the worst case for the cancellation of any offset
+    carried through the fp32 sums. Also with the residual epilogue."""
+    r = rng(50)
+    K, N = 14336, 1024
+    W, s = q8(O, h16(r, N, K, sd=0.02))
+    for M in [1, 5, 8]:
+        x = (np.abs(r.standard_normal((M, K))) * 0.7 + 0.05).astype(np.float16)
+        spikes = r.choice(K, 24, replace=False)
+        x[:, spikes] = (r.random((M, 24)) * 60 + 40).astype(np.float16)
+        got = host(hi.gemv(cuda(x), cuda(W), scales=cuda(s)))
+        check(f"int8 positive x K={K} M={M}", got, O.gemv(x, W, scales=s), 2e-3, 2e-3)
+        res = h16(r, M, N)
+        out = cuda(res)
+        hi.gemv(cuda(x), cuda(W), out=out, epi=1, scales=cuda(s))
+        check(f"int8 positive x residual M={M}", host(out), O.gemv(x, W, out=res.copy(), epi=1, scales=s), 4e-3, 2e-3)

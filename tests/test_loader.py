@@ -241,11 +241,13 @@ def test_verify_is_bit_identical_to_greedy_decode(hi, O, tmp_path, kind):
     a = hi.Engine(path, max_batch=2, max_seq=80, max_prefill=32)
     b = hi.Engine(path, max_batch=2, max_seq=80, max_prefill=32)
     try:
-        assert a.MAX_VERIFY == 8
+        assert a.MAX_VERIFY == 16  # the reference's kGemvMaxRows (api.cu:156, 2066)
         p0 = len(prompt)
         first = a.prefill(0, prompt)
         assert b.prefill(0, prompt) == first
-        for R, graph in [(1, False), (5, False), (8, True), (8, True), (3, True)]:
+        # 9..16 rows run the fused-norm projections as two launches; every row stays bit-identical
+        for R, graph in [(1, False), (5, False), (8, True), (8, True), (3, True), (9, False), (12, True), (16, True),
+                         (16, True), (16, False)]:
             draft = [first] + r.integers(0, C["V"], R - 1).tolist()
             toks, lg = a.verify(0, draft, p0, graph=graph, logits=True)
             lg = host(lg)
@@ -262,7 +264,7 @@ def test_verify_is_bit_identical_to_greedy_decode(hi, O, tmp_path, kind):
         b.decode(1, 4, graph=False)
         assert a.history(0, p0 + 1, 4) == b.history(0, p0 + 1, 4)
         with pytest.raises(ValueError):
-            a.verify(0, [1] * 9, p0)  # more rows than hi_verify_max_rows
+            a.verify(0, [1] * 17, p0)  # more rows than hi_verify_max_rows
     finally:
         a.close()
         b.close()

@@ -90,8 +90,8 @@ def test_moe_grouped_path_graph_replay(hi, O):
     work = torch.empty(hi.lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device="cuda")
 
     def run():
-        hi._ok(hi.lib.hi_moe_experts(hi._p(xn_d), H, hi._p(wgu_d), hi._p(wdn_d), hi._p(idx_d), hi._p(w_d), M, E, k, H, I,
-                                     flags, 0.22, hi._p(x), H, 2, hi._p(work), hi._s()), "moe_experts")
+        hi.check_rc(hi.lib.hi_moe_experts(hi.ptr(xn_d), H, hi.ptr(wgu_d), hi.ptr(wdn_d), hi.ptr(idx_d), hi.ptr(w_d), M, E, k, H, I,
+                                     flags, 0.22, hi.ptr(x), H, 2, hi.ptr(work), hi.cur_stream()), "moe_experts")
     run()
     torch.cuda.synchronize()
     check("grouped eager", host(x), ref, 4e-3, 4e-3)
@@ -173,8 +173,8 @@ def test_moe_route_experts_graph_replay(hi):
     work = torch.empty(hi.lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device="cuda")
 
     def run():
-        hi._ok(hi.lib.hi_moe_route_experts(hi._p(xn), H, hi._p(Wr), hi._p(wgu), hi._p(wdn), M, E, k, H, I, flags, 0.22,
-                                           hi._p(x), H, hi._p(idx), hi._p(w), hi._p(work), hi._s()), "moe_route_experts")
+        hi.check_rc(hi.lib.hi_moe_route_experts(hi.ptr(xn), H, hi.ptr(Wr), hi.ptr(wgu), hi.ptr(wdn), M, E, k, H, I, flags, 0.22,
+                                           hi.ptr(x), H, hi.ptr(idx), hi.ptr(w), hi.ptr(work), hi.cur_stream()), "moe_route_experts")
     run()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
