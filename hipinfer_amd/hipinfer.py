@@ -27,6 +27,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.abspath(os.environ.get("HIPINFER_LIB", os.path.join(_HERE, "libhipinfer.so")))
 if not os.path.exists(LIBRARY_PATH):
     raise ImportError(f"hipinfer_amd: {LIBRARY_PATH} is not built; run `python -m hipinfer_amd.build`")
+# torch ships its own HIP runtime and this library links the system one; the two share the process
+# only when torch's is initialised first, so make sure it is before the library is loaded
+torch.cuda.is_available()
 lib = ctypes.CDLL(LIBRARY_PATH)
 
 # moe_flags bits (the reference's MOE_NORM_TOPK / MOE_FP16_WEIGHTS): softmax over the chosen k

@@ -58,20 +58,15 @@ def gemm_check(hi, O, name, A, W, r, epi=0, bias=None, scales=None, res=None, to
     torch.cuda.synchronize()
 
 
-def _num_configs():
-    """The library's tile-config count (a constant; reading it needs no GPU)."""
-    import ctypes
-    import os
-    so = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "hipinfer_amd", "libhipinfer.so")
-    try:
-        return ctypes.CDLL(so).hi_gemm_num_configs()
-    except OSError:
-        return 19
-
-
-NUM_CFGS = _num_configs()
+# The library's tile-config count. Not read from the library at collection time: libhipinfer.so must
+# be loaded after torch has initialised its HIP runtime. test_config_count_is_current keeps it honest.
+NUM_CFGS = 19
 # every tile configuration, and the automatic choice (-1)
 CFGS = list(range(-1, NUM_CFGS))
+
+
+def test_config_count_is_current(hi):
+    assert hi.lib.hi_gemm_num_configs() == NUM_CFGS, "update NUM_CFGS: every config must be tested"
 
 
 def need_cfg(hi, cfg):
