@@ -113,7 +113,7 @@ int ensure_ws(size_t bytes, hipStream_t s, bool* ok) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s);
+int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s, float* fixed_ws = nullptr);
 
 // First-call autotuning per (M bucket, N, K, SwiGLU, int8) and device, as the reference's
 // gemm_choose (api.cu:465-552): every valid (tile, split) is timed on the real activations into a
@@ -231,8 +231,9 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
 }
 
 // Launch with a chosen (tile, split): sets up the split-K workspace (or falls back to one split
-// when it would have to grow inside stream capture).
-int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s) {
+// when it would have to grow inside stream capture). With fixed_ws the partials go there instead,
+// and the caller has checked that they fit.
+int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s, float* fixed_ws) {
   const HiDevice* d = hi_device();
   if (!d) return -2;
   GemmArgs g = g0;
@@ -244,14 +245,18 @@ int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s
   const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
   if (ch.splits > 1) {
     bool ok = false;
-    if (tiles <= kMaxTiles) {
+    if (tiles <= kMaxTiles && fixed_ws) {
+      ok = true;
+      g.ws = fixed_ws;
+    } else if (tiles <= kMaxTiles) {
       const int r = ensure_ws((size_t)ch.splits * g.M * g.N * sizeof(float), s, &ok);
       if (r) return r;
+      if (ok) {
+        std::lock_guard<std::mutex> lk(g_ws_mu);
+        g.ws = g_ws[d->id].ws;
+      }
     }
-    if (ok) {
-      std::lock_guard<std::mutex> lk(g_ws_mu);
-      g.ws = g_ws[d->id].ws;
-    } else {
+    if (!ok) {
       ch.splits = 1;
       kps = nkt;
     }
@@ -266,10 +271,9 @@ int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s
 }
 
 
-int gemm_entry(const void* A, int lda, const void* W, const void* scales, const void* bias, void* C, int ldc, int M,
-               int N, int K, int epi, void* stream, const char* who) {
-  const HiDevice* d = hi_device();
-  if (!d) return -2;
+// Shape and pointer checks shared by the entry points; fills g. Returns 0, or a negative code.
+int gemm_args(const void* A, int lda, const void* W, const void* scales, const void* bias, void* C, int ldc, int M,
+              int N, int K, int epi, const char* who, GemmArgs& g) {
   if (epi < 0 || epi > 2) HI_FAIL("%s: epi must be 0, 1 or 2 (got %d)", who, epi);
   if (M < 0 || N < 16 || K < 32 || K % 32 || N % (epi == 2 ? 32 : 16))
     HI_FAIL("%s: unsupported shape M=%d N=%d K=%d epi=%d (K %% 32 == 0, N %% %d == 0)", who, M, N, K, epi,
@@ -280,10 +284,7 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
   if (!aligned(W, 16)) HI_FAIL("%s: W must be 16-byte aligned", who);
   const int n_out = epi == 2 ? N / 2 : N;
   if (ldc < n_out) HI_FAIL("%s: ldc %d < %d output columns", who, ldc, n_out);
-  const bool q8 = scales != nullptr;
-  const hipStream_t s = (hipStream_t)stream;
-
-  GemmArgs g{};
+  g = GemmArgs{};
   g.A = (const f16*)A;
   g.lda = lda;
   g.W = W;
@@ -295,6 +296,18 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
   g.N = N;
   g.K = K;
   g.vec_c = aligned(C, 8) && ldc % 4 == 0;
+  return 0;
+}
+
+int gemm_entry(const void* A, int lda, const void* W, const void* scales, const void* bias, void* C, int ldc, int M,
+               int N, int K, int epi, void* stream, const char* who) {
+  const HiDevice* d = hi_device();
+  if (!d) return -2;
+  GemmArgs g;
+  if (int r = gemm_args(A, lda, W, scales, bias, C, ldc, M, N, K, epi, who, g)) return r;
+  if (M == 0) return 0;
+  const bool q8 = scales != nullptr;
+  const hipStream_t s = (hipStream_t)stream;
   Choice ch{1, 1};
   if (g_force_cfg >= 0 && g_force_cfg < kGemmNumCfgs && gemm_cfg_fits(g_force_cfg, q8, K)) {  // else: automatic
     ch = gemm_pick(M, N, K, q8, d->cus);
@@ -307,6 +320,79 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------- the entry point that allocates nothing
+// hi_gemm_noalloc keeps its split-K partials in this file-scope device array instead of the
+// workspace hi_gemm grows with hipMalloc. Each GPU the library runs on holds its own 64 MB copy
+// from the first launch until the process ends. In host code `scratch` is only the host-side
+// handle of the array: its device address on the current GPU comes from hipGetSymbolAddress and
+// is kept per device in g_scratch, and only that address is ever given to a kernel.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+namespace {
+std::mutex g_scratch_mu;
+float* g_scratch[64] = {};
+
+// The current device's copy of `scratch`, looked up once per device (with that device current).
+float* scratch_on(const HiDevice* d) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[d->id]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fprintf(stderr, "hipinfer_amd: hipGetSymbolAddress(scratch) failed on device %d: %s\n", d->id,
+              hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch[d->id] = (float*)p;
+  }
+  return g_scratch[d->id];
+}
+}  // namespace
+
+// C (epi) A[M, K] @ W[N, K]^T like hi_gemm (scales == NULL) or hi_gemm_w8 (scales given), without any
+// allocation: no hipMalloc / hipFree, no first-call autotuning (which times candidates on scratch
+// copies). The tile is the one the autotuner already chose for this shape on this device, else the
+// cost model's, or a forced one (hi_gemm_force_config / hi_gemm_force_splits); split-K partials
+// ([splits][M][N] fp32) live in the library's 64 MB static scratch. An automatic split is lowered
+// until its partials fit; a forced split that does not fit is rejected (-1). Every call on a GPU
+// shares that GPU's scratch: calls that overlap in time on one GPU (two streams, two host threads)
+// race. Every partial is written before it is read, so nothing needs clearing between calls.
+HI_EXPORT int hi_gemm_noalloc(const void* A, int lda, const void* W, const void* scales, const void* bias, void* C,
+                              int ldc, int M, int N, int K, int epi, void* stream) {
+  const char* who = "hi_gemm_noalloc";
+  const HiDevice* d = hi_device();
+  if (!d) return -2;
+  GemmArgs g;
+  if (int r = gemm_args(A, lda, W, scales, bias, C, ldc, M, N, K, epi, who, g)) return r;
+  if (M == 0) return 0;
+  float* ws = scratch_on(d);
+  if (!ws) return -2;
+  const bool q8 = scales != nullptr;
+  Choice ch = gemm_pick(M, N, K, q8, d->cus);
+  if (g_force_cfg >= 0 && g_force_cfg < kGemmNumCfgs && gemm_cfg_fits(g_force_cfg, q8, K)) {
+    ch.cfg = g_force_cfg;
+  } else {
+    int mb = 16;
+    while (mb < M && mb < 4096) mb *= 2;
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    auto it = g_tuned.find(std::make_tuple(d->id, mb, N, K, epi == 2, q8));
+    if (it != g_tuned.end()) ch = it->second;
+  }
+  const size_t per_split = (size_t)M * N * sizeof(float);
+  if (g_force_splits >= 1) {
+    ch.splits = g_force_splits;
+    const int nkt = (K + kGemmCfgs[ch.cfg].bk - 1) / kGemmCfgs[ch.cfg].bk;
+    const int sp = std::min(ch.splits, nkt);
+    if (sp > 1 && (size_t)sp * per_split > kScratchBytes)
+      HI_FAIL("%s: %d splits of %d x %d fp32 partials need %zu bytes, over the %zu-byte static scratch", who, sp, M, N,
+              (size_t)sp * per_split, kScratchBytes);
+  } else {
+    while (ch.splits > 1 && (size_t)ch.splits * per_split > kScratchBytes) ch.splits--;
+  }
+  return launch_choice(g, ch, epi, q8, (hipStream_t)stream, ws);
+}
 
 // C (epi) A[M, K] @ W[N, K]^T (+ bias[N] for epi 0 when non-null), fp16 weights.
 HI_EXPORT int hi_gemm(const void* A, int lda, const void* W, const void* bias, void* C, int ldc, int M, int N, int K,

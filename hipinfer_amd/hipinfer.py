@@ -57,6 +57,8 @@ int hi_gemm_force_splits(int splits);
 int hi_gemm_num_configs();
 int hi_gemm_config_desc(int cfg, str out, int n);
 int hi_gemm_last_choice(ptr cfg, ptr splits);
+int hi_gemm_noalloc(ptr A, int lda, ptr W, ptr scales, ptr bias, ptr C, int ldc, int M, int N, int K, int epi,
+                    ptr stream);
 int hi_moe_router(ptr xn, int ldx, ptr Wr, int M, int E, int H, int k, int flags, ptr idx, ptr w, ptr stream);
 size hi_moe_work_bytes(int M, int k, int E, int H, int I);
 int hi_moe_experts(ptr xn, int ldxn, ptr wgu, ptr wdown, ptr idx, ptr w, int M, int E, int k, int H, int I, int flags,
@@ -233,6 +235,21 @@ def gemm(A, W, out=None, epi=0, bias=None, scales=None):
     tail = (ptr(bias), ptr(out), out.stride(0), M, N, K, epi, cur_stream())
     rc = lib.hi_gemm_w8(*head, ptr(scales), *tail) if q8 else lib.hi_gemm(*head, *tail)
     check_rc(rc, "gemm")
+    return out
+
+
+def gemm_noalloc(A, W, out, epi=0, bias=None, scales=None):
+    """gemm into a caller-provided `out` through the library's entry point that allocates no device
+    memory (safe under graph capture and in allocation-free loops): split-K partials use the
+    library's 64 MB static scratch, the tile comes from earlier tuning or the cost model. Calls that
+    overlap in time on one GPU race on that scratch."""
+    _need("gemm_noalloc", A, torch.float16, 2, rows=True)
+    _weight("gemm_noalloc", W, scales)
+    _need("gemm_noalloc", bias, torch.float16, 1, optional=True)
+    _need("gemm_noalloc", out, torch.float16, 2, rows=True)
+    M, K = A.shape
+    check_rc(lib.hi_gemm_noalloc(ptr(A), A.stride(0), ptr(W), ptr(scales), ptr(bias), ptr(out), out.stride(0), M,
+                                 W.shape[0], K, epi, cur_stream()), "gemm_noalloc")
     return out
 
 

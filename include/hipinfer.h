@@ -70,6 +70,17 @@ int hi_gemm_config_desc(int cfg, char* out, int n);
  * that did not fit the shape or weight format and fell back to the automatic choice. */
 int hi_gemm_last_choice(int* cfg, int* splits);
 
+/* hi_gemm (scales == NULL) or hi_gemm_w8 (scales given) for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * No counterpart in the reference. It allocates nothing and never autotunes. The tile is the one the
+ * autotuner already chose for the shape on this GPU, else the cost model's, or a forced one. Split-K
+ * partials live in a 64 MB static device array per GPU, which the GPU holds until the process
+ * ends. An automatic split count is lowered until its splits * M * N fp32 partials fit; a forced
+ * split count that does not fit is rejected (-1). Calls that overlap in time on one GPU share that
+ * array and race. Returns 0, -1 (bad argument, reason on stderr) or -2 (HIP error). */
+int hi_gemm_noalloc(const void* A, int lda, const void* W, const void* scales, const void* bias, void* C, int ldc,
+                    int M, int N, int K, int epi, void* stream);
+
 /* ---- mixture of experts (fp16 experts, E <= 256, k <= 16)
  * Router + top-k of M normalised rows xn[M, H] under Wr[E, H]: idx[M, k] int, w[M, k] fp32, descending;
  * flags bit 0 = softmax over the k (else over all E), bit 1 = weights rounded to fp16.
