@@ -321,10 +321,18 @@ def prefill_bench(torch, hi, steps, warmup, q8_too):
             g = capture(torch, lambda: pm.layer_pass(b, q8))
             ms, _ = time_graph(torch, g, max(3, steps // 2), warmup)
             us = ms * 1e3 / P_L
+            # HBM bytes a layer must move at least: its weights (int8: + row scales), A in, C out
+            # (and the residual read for o / down)
+            wb = sum(N * K * (1 if q8 else 2) + (2 * N if q8 else 0) for N, K in P_SHAPES.values())
+            ab = 2 * M * (P_SHAPES["qkv"][1] + P_SHAPES["o"][1] + P_SHAPES["gate_up"][1] + P_SHAPES["down"][1])
+            cb = 2 * M * (P_SHAPES["qkv"][0] + 2 * P_SHAPES["o"][0] + P_SHAPES["gate_up"][0] // 2 + 2 * P_SHAPES["down"][0])
+            hbm_us = (wb + ab + cb) / (HBM_PEAK_GBS * 1e3)
             res["layers"][f"M{M}_{tag}"] = {"us_per_layer": round(us, 2),
                                             "TFLOP/s": round(flops_layer(M) / (us * 1e-6) / 1e12, 1),
                                             "pct_mfma_peak": round(100 * flops_layer(M) / (us * 1e-6) / 1e12
-                                                                   / MFMA_F16_PEAK_TFLOPS, 1)}
+                                                                   / MFMA_F16_PEAK_TFLOPS, 1),
+                                            "hbm_floor_us": round(hbm_us, 2),
+                                            "pct_hbm_ceiling": round(100 * hbm_us / us, 1)}
             del g
         b = pm.buffers(1024)
         for kind in P_SHAPES:
@@ -366,47 +374,139 @@ def time_graph(torch, g, steps, warmup):
     return e0.elapsed_time(e1) / steps, wall / steps
 
 
-def cpu_baseline(torch, model, budget_s=12.0):
-    """The oracle's restatement of the reference's CPU path (fp16(fp32-or-better x @ W^T) with the
-    same epilogues) on one Llama-3.1-8B layer's four GEMVs (fp16 weights copied from the GPU),
-    repeated for about budget_s seconds on the host's cores. Returns GB/s of weight bytes."""
+def _cpu_layer(torch, dims, layer, q8_layer, n1, n2, seed):
+    """One decode layer's weights on the host for the CPU legs: fp16 (or int8 + fp16 row scales) as
+    the GPU streams them, and the fp32 copies the reference's CPU engine computes with (RefEngine
+    holds fp32 weights; int8 as q * s in fp32, tests/test_kernels.py:389-390)."""
+    import numpy as np
+    H, Hq, Hkv, D, I = dims
+    host = {k: v.cpu().numpy() for k, v in layer.items()}
+    q8 = {k: (q.cpu().numpy(), s.cpu().numpy()) for k, (q, s) in q8_layer.items()}
+    f32 = {k: torch.from_numpy(v.astype(np.float32)) for k, v in host.items()}
+    f32q = {k: torch.from_numpy(q.astype(np.float32) * s.astype(np.float32)[:, None]) for k, (q, s) in q8.items()}
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((1, H)).astype(np.float16)
+    return {"dims": dims, "fp16": host, "int8": q8, "f32": {"fp16": f32, "int8": f32q}, "x": x,
+            "n1": n1.cpu().numpy(), "n2": n2.cpu().numpy()}
+
+
+def _torch_layer(torch, L, fmt, eps=1e-5):
+    """The reference's CPU path for one decode layer, restated in torch (scripts/ref_engine.py: mm =
+    fp16(fp32 x @ W^T), 141-143; rmsnorm 145-147; swiglu / deinterleave 32-42; RoPE in fp16 ops):
+    QKV (+ RoPE on q, k), o + residual (the q columns stand in for the attention output, as on the
+    GPU), gate/up + SwiGLU, down + residual."""
+    H, Hq, Hkv, D, I = L["dims"]
+    W = L["f32"][fmt]
+    r = lambda t: t.half().float()
+    x = torch.from_numpy(L["x"]).float()
+    n1, n2 = torch.from_numpy(L["n1"]).float(), torch.from_numpy(L["n2"]).float()
+    rms = lambda v, w: r(w * r(v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + eps)))
+    qkv = r(rms(x, n1) @ W["qkv"].T)
+    hd = D // 2
+    qk = qkv[:, :(Hq + Hkv) * D].view(1, Hq + Hkv, 2, hd)
+    c, sn = torch.full((hd,), 0.6), torch.full((hd,), 0.8)
+    a, b = qk[:, :, 0], qk[:, :, 1]
+    rot = torch.stack([r(r(a * c) - r(b * sn)), r(r(b * c) + r(a * sn))], 2)
+    q = rot.view(1, -1)[:, :Hq * D]
+    x = r(x + r(q @ W["o"].T))
+    gu = r(rms(x, n2) @ W["gate_up"].T).view(1, -1, 2, 16)
+    g, u = gu[:, :, 0].reshape(1, I), gu[:, :, 1].reshape(1, I)
+    g, u = r(g), r(u)
+    act = r(r(g * torch.sigmoid(g)) * u)
+    x = r(x + r(act @ W["down"].T))
+    return x
+
+
+def _c_layer(O, L, fmt):
+    """The same layer through the C restatement (oracle/hi_oracle.c: fp64-or-better sums with the
+    reference's fp16 rounding points)."""
+    import numpy as np
+    H, Hq, Hkv, D, I = L["dims"]
+    Wd = L[fmt]
+    w = (lambda k: (Wd[k], None)) if fmt == "fp16" else (lambda k: Wd[k])
+    xs = L["x"].copy()
+    S = 16
+    hd = D // 2
+    cs = np.stack([np.full((S, hd), 0.6), np.full((S, hd), 0.8)], -1).astype(np.float16)
+    kc = np.zeros((1, Hkv, S, D), np.float16)
+    vc = np.zeros_like(kc)
+    q = np.zeros((1, Hq * D), np.float16)
+    act = np.zeros((1, I), np.float16)
+    Wq, sq = w("qkv")
+    O.gemv_qkv_rope(xs, Wq, L["n1"], Hq, Hkv, cs, np.array([3], np.int32), kc, vc, q, scales=sq)
+    Wo, so = w("o")
+    O.gemv(q, Wo, out=xs, epi=1, scales=so)
+    Wg, sg = w("gate_up")
+    O.gemv(xs, Wg, out=act, normw=L["n2"], epi=2, scales=sg)
+    Wdn, sdn = w("down")
+    O.gemv(act, Wdn, out=xs, epi=1, scales=sdn)
+    return xs
+
+
+def _median_time(fn, runs=5, min_s=0.0):
+    fn()  # warm-up (page-ins, thread pools)
+    times = []
+    t_end = time.perf_counter() + min_s
+    while len(times) < runs or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(torch, model):
+    """The reference's CPU path timed on this host's cores, on the decode GEMV set of one layer of
+    C2 (Llama-3.1-8B) and of C1 (TinyLlama-1.1B), fp16 and int8 weights, M = 1:
+      * torch: the reference's own CPU engine restated in torch float32 (weights held in fp32, as
+        RefEngine holds them; int8 as fp32 q * s), torch.get_num_threads() threads;
+      * C: oracle/hi_oracle.c, the build's C restatement, with OpenMP on the job's core share and on
+        one core.
+    Each figure is the median of at least 5 runs; rates are the GPU format's weight bytes (what the
+    GPU GEMVs stream) per second. `value` is the torch leg on C2 fp16."""
     import numpy as np
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import oracle as O
 
     try:
-        cores = len(os.sched_getaffinity(0))
+        share = len(os.sched_getaffinity(0))
     except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", "16"))))
-    O.set_threads(cores)
-    ly = model.layers[0]
-    Wh = {k: ly[k].cpu().numpy() for k in SHAPES}
-    n1, n2 = ly["n1"].cpu().numpy(), ly["n2"].cpu().numpy()
-    cs, pos = model.cs.cpu().numpy(), np.array([7], np.int32)
-    rng = np.random.default_rng(SEED)
-    x = rng.standard_normal((1, H)).astype(np.float16)
-    kc = np.zeros((1, HKV, model.max_seq, D), np.float16)
-    vc = np.zeros_like(kc)
-    q = np.zeros((1, HQ * D), np.float16)
-    act = np.zeros((1, I), np.float16)
-    nbytes = sum(N * K * 2 for N, K in SHAPES.values())
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 2:
-        xs = x.copy()
-        t0 = time.perf_counter()
-        O.gemv_qkv_rope(xs, Wh["qkv"], n1, HQ, HKV, cs, pos, kc, vc, q)
-        O.gemv(q, Wh["o"], out=xs, epi=1)
-        O.gemv(xs, Wh["gate_up"], out=act, normw=n2, epi=2)
-        O.gemv(act, Wh["down"], out=xs, epi=1)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": O.get_threads(), "kind": "port",
-            "sample": f"one Llama-3.1-8B layer's 4 decode GEMVs (QKV+RoPE, o+res, gate/up+SwiGLU, down+res; "
-                      f"{nbytes / 1e6:.1f} MB fp16 weights, M=1), oracle/hi_oracle.c with OpenMP, median of "
-                      f"{len(times)} repetitions ({sum(times):.1f} s)"}
+        share = os.cpu_count() or 1
+    # the pool gives each one-GPU job a 16-core share (OMP_NUM_THREADS on the GPU box)
+    share = max(1, min(share, int(os.environ.get("OMP_NUM_THREADS", str(share)))))
+    tthreads = torch.get_num_threads()
+    g = _seeded(torch, SEED + 20)
+    c1_dims = (2048, 32, 4, 64, 5632)
+    c1_shapes = {"qkv": ((32 + 8) * 64, 2048), "o": (2048, 2048), "gate_up": (2 * 5632, 2048), "down": (2048, 5632)}
+    c1 = {k: _w(torch, g, *sh) for k, sh in c1_shapes.items()}
+    c1q = {k: model.hi.quantize_rows(v) for k, v in c1.items()}
+    nrm = lambda n: (torch.rand(n, generator=g, device="cuda") + 0.5).half()
+    layers = {
+        "C2": _cpu_layer(torch, (H, HQ, HKV, D, I), {k: model.layers[0][k] for k in SHAPES}, model.q8[0],
+                         model.layers[0]["n1"], model.layers[0]["n2"], SEED + 21),
+        "C1": _cpu_layer(torch, c1_dims, c1, c1q, nrm(2048), nrm(2048), SEED + 22),
+    }
+    legs = {}
+    for name, L in layers.items():
+        for fmt in ("fp16", "int8"):
+            nbytes = sum(v.size * v.itemsize for v in L["fp16"].values()) if fmt == "fp16" else \
+                sum(q.size + s.size * 2 for q, s in L["int8"].values())
+            with torch.no_grad():
+                t, n = _median_time(lambda: _torch_layer(torch, L, fmt))
+            legs[f"torch_{name}_{fmt}"] = {"GB/s": round(nbytes / t / 1e9, 3), "ms": round(t * 1e3, 3),
+                                           "threads": tthreads, "runs": n}
+            for cores in (share, 1):
+                O.set_threads(cores)
+                t, n = _median_time(lambda: _c_layer(O, L, fmt))
+                legs[f"c_{name}_{fmt}_{cores}core"] = {"GB/s": round(nbytes / t / 1e9, 3), "ms": round(t * 1e3, 3),
+                                                       "threads": O.get_threads(), "runs": n}
+    head = legs["torch_C2_fp16"]
+    return {"value": head["GB/s"], "unit": "GB/s", "cores": tthreads, "kind": "port",
+            "sample": "one Llama-3.1-8B layer's decode GEMVs (QKV+RoPE, o+res, gate/up+SwiGLU, down+res; "
+                      "436.2 MB of fp16 weights, M = 1) through the reference's CPU engine restated in torch "
+                      "float32 (scripts/ref_engine.py mm/rmsnorm/swiglu), median of >= 5 runs; legs: the same "
+                      "for int8 and for a TinyLlama layer, and oracle/hi_oracle.c on %d cores and on 1 core" % share,
+            "legs": legs}
 
 
 # ------------------------------------------------------------------ the other BASELINE configs
@@ -547,7 +647,124 @@ def traffic_from_profile():
     return None
 
 
+def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
+    """A plain device-to-device copy of nbytes (torch's copy kernel), timed with HIP events: bytes
+    read plus bytes written per second, the practical HBM rate next to the 8 TB/s datasheet figure."""
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"GB/s": round(2 * nbytes / us / 1e3, 1), "bytes_moved": 2 * nbytes, "us": round(us, 2),
+            "pct_hbm_peak": round(100 * 2 * nbytes / us / 1e3 / HBM_PEAK_GBS, 1)}
+
+
+def timeline(csv_path):
+    """Per-kind durations and launch gaps of replayed decode tokens, from a rocprofv3 kernel trace
+    (`--kernel-trace --output-format csv`) of `bench.py --profile token` / `token8`. A token is the
+    run of 129 GEMV launches (32 x [QKV, o, gate/up, down] + lm_head); each GEMV is named by its
+    epilogue (template argument 3: 3 QKV+RoPE, 1 residual, 2 SwiGLU, 0 lm_head), and the residual
+    launch after QKV is o, after gate/up down. The gap of a launch is the time from the previous
+    launch's end to its start. Prints a markdown table."""
+    import csv
+    import re
+    rows = []
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            m = re.search(r"gemv\w*<\s*(\d+),\s*(true|false),\s*(\d+)", name)
+            if m:
+                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), int(m.group(3))))
+    rows.sort()
+    per_token = 32 * 4 + 1
+    tokens = [rows[i:i + per_token] for i in range(0, len(rows) - per_token + 1, per_token)]
+    tokens = [t for t in tokens if [e for _, _, e in t[:4]] == [3, 1, 2, 1] and t[-1][2] == 0]
+    tokens = tokens[2:] if len(tokens) > 3 else tokens  # skip the eager pass and the first replay
+    stats = {}
+    spans = []
+    for t in tokens:
+        spans.append((t[-1][1] - t[0][0]) / 1e3)
+        prev_end, prev_kind = None, None
+        for start, end, epi in t:
+            kind = {3: "qkv", 2: "gate_up", 0: "lm_head"}.get(epi) or ("o" if prev_kind == "qkv" else "down")
+            d = stats.setdefault(kind, [0, 0.0, 0.0])
+            d[0] += 1
+            d[1] += (end - start) / 1e3
+            if prev_end is not None:
+                d[2] += (start - prev_end) / 1e3
+            prev_end, prev_kind = end, kind
+    n = len(tokens)
+    print(f"tokens analysed: {n}; token span (first launch start to last launch end): "
+          f"{sum(spans) / n:.1f} us (min {min(spans):.1f}, max {max(spans):.1f})")
+    print("| kind | launches per token | avg duration us | avg gap before us | per token: busy us | gaps us |")
+    print("|---|---|---|---|---|---|")
+    tb = tg = 0.0
+    for kind in ["qkv", "o", "gate_up", "down", "lm_head"]:
+        c, dur, gap = stats[kind]
+        per = c // n
+        tb += dur / n
+        tg += gap / n
+        print(f"| {kind} | {per} | {dur / c:.2f} | {gap / c:.2f} | {dur / n:.1f} | {gap / n:.1f} |")
+    print(f"| all | {per_token} | | | {tb:.1f} | {tg:.1f} |")
+
+
+def gemm_counters(csv_path, cus=256, xcds=8, replays=3):
+    """Per-GEMM-kind counters of the last `replays` layer passes of `bench.py --profile gemm`, from a
+    rocprofv3 `--pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_BUSY_CYCLES
+    SQ_WAVE_CYCLES SQ_WAIT_INST_ANY` counter CSV: MfmaUtil = 100 * SQ_VALU_MFMA_BUSY_CYCLES /
+    (GRBM_GUI_ACTIVE * CUs * 4), rocprofv3's own derived metric, with GRBM_GUI_ACTIVE taken per XCD
+    (the raw counter is the sum of the 8 XCDs' copies). A pass is 28 layers x (QKV, o, gate/up,
+    down) GEMM launches, in that order. Prints a markdown table."""
+    import csv
+    disp = {}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            if "gemm_kernel" not in r["Kernel_Name"]:
+                continue
+            d = disp.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"]})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    ids = sorted(disp)
+    per_pass = P_L * 4
+    last = ids[-replays * per_pass:]
+    kinds = ["qkv", "o", "gate_up", "down"]
+    agg = {k: {"n": 0} for k in kinds}
+    for i, d_id in enumerate(last):
+        a = agg[kinds[i % 4]]
+        a["n"] += 1
+        a["name"] = disp[d_id]["name"]
+        for c, v in disp[d_id].items():
+            if c != "name":
+                a[c] = a.get(c, 0.0) + v
+    print(f"dispatches: {len(ids)} gemm_kernel launches in the trace; the last {len(last)} ({replays} passes) used")
+    print("| GEMM | kernel | MfmaUtil % | MFMA flop per launch (MOPs x 512) | SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES % "
+          "| GPU-active cycles per launch (per XCD) |")
+    print("|---|---|---|---|---|---|")
+    for k in kinds:
+        a = agg[k]
+        active = a.get("GRBM_GUI_ACTIVE", 0) / xcds
+        util = 100 * a.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) / max(1.0, active * cus * 4)
+        wait = 100 * a.get("SQ_WAIT_INST_ANY", 0) / max(1.0, a.get("SQ_WAVE_CYCLES", 0))
+        name = a.get("name", "")
+        name = name[name.find("gemm_kernel"):][:60]
+        print(f"| {k} | `{name}` | {util:.1f} | {a.get('SQ_INSTS_VALU_MFMA_MOPS_F16', 0) * 512 / a['n']:.4g} | "
+              f"{wait:.1f} | {active / a['n']:.0f} |")
+
+
 def main():
+    if len(sys.argv) == 3 and sys.argv[1] == "--timeline":
+        timeline(sys.argv[2])
+        return
+    if len(sys.argv) == 3 and sys.argv[1] == "--gemm-counters":
+        gemm_counters(sys.argv[2])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -668,6 +885,14 @@ def main():
     if not args.no_gemm:
         log("prefill GEMM ...")
         res["prefill_gemm"] = prefill_bench(torch, hi, args.steps, args.warmup, not args.no_int8)
+        gk = res["prefill_gemm"]["kernels_m1024"]["gate_up_fp16"]
+        flops = 2.0 * 1024 * gk["N"] * gk["K"]
+        res["roofline_mfma"] = {
+            "bound": "mfma", "achieved": gk["TFLOP/s"], "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(gk["TFLOP/s"] / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": "gemm_kernel (tuned tile) gate/up + SwiGLU, Llama-3.2-3B, M=1024, N=16384, K=3072, fp16",
+            "launch_flops": flops, "avg_us": gk["us"],
+            "counters": "profiles/gemm_prefill_llama32_3b.md (rocprofv3 MfmaUtil per GEMM kind)"}
     if not args.no_configs:
         del g16
         if "int8" in out:
@@ -681,6 +906,7 @@ def main():
                                                   [1, 2, 5, 8], 28, args.steps, SEED + 11, bias=True),
             "C5_granite_moe": moe_bench(torch, hi, args.steps, SEED + 12),
         }
+    res["copy_bandwidth"] = copy_bandwidth(torch)
     if not args.no_cpu:
         log("cpu baseline ...")
         res["cpu_baseline"] = cpu_baseline(torch, model)
