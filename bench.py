@@ -601,7 +601,7 @@ def moe_bench(torch, hi, steps, seed):
         xn = torch.randn(M, H, generator=g, device="cuda").half()
         x0 = torch.randn(M, H, generator=g, device="cuda").half()
         x = x0.clone()
-        work = torch.empty(hi.lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device="cuda")
+        work = torch.zeros(hi.lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device="cuda")
         idx = torch.empty(M, k, dtype=torch.int32, device="cuda")
         wts = torch.empty(M, k, dtype=torch.float32, device="cuda")
 

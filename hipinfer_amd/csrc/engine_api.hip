@@ -509,13 +509,14 @@ Engine* load(const char* path, int maxB, int max_seq, int max_pf) {
     ok = (e->moe_idx = (int*)dalloc(e, M * c.top_k * 4)) && (e->moe_w = (float*)dalloc(e, M * c.top_k * 4)) &&
          (e->moe_work = dalloc(e, hi_moe_work_bytes((int)M, c.top_k, c.n_experts, H, I)));
   if (!ok) return fail2();
-  // zeroed state (the decode work buffer's counters must start at zero); caches too, so an
+  // zeroed state (the decode and MoE work buffers' counters must start consistent); caches too, so an
   // unwritten position reads as zero, never as stale memory
   ok = hipMemsetAsync(e->kc, 0, e->layer_cache * c.layers * 2, e->st) == hipSuccess &&
        hipMemsetAsync(e->vc, 0, e->layer_cache * c.layers * 2, e->st) == hipSuccess &&
        hipMemsetAsync(e->work, 0, hi_decode_work_bytes(maxB, Hq, Hkv, D), e->st) == hipSuccess &&
        hipMemsetAsync(e->tok, 0, maxB * 4, e->st) == hipSuccess && hipMemsetAsync(e->pos, 0, maxB * 4, e->st) == hipSuccess &&
-       hipMemsetAsync(e->hist, 0, (size_t)maxB * max_seq * 4, e->st) == hipSuccess;
+       hipMemsetAsync(e->hist, 0, (size_t)maxB * max_seq * 4, e->st) == hipSuccess &&
+       (!c.moe || hipMemsetAsync(e->moe_work, 0, hi_moe_work_bytes((int)M, c.top_k, c.n_experts, H, I), e->st) == hipSuccess);
   if (!ok) return fail2();
   // RoPE table as HF computes it: fp32 inv_freq (from the export) times the fp32 position, cos and
   // sin of that fp32 angle times attention_scaling, rounded to fp16 (api.cu:1421-1431)

@@ -61,18 +61,21 @@ __device__ __forceinline__ float dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
-// Sum over the 64 lanes of a wave; every lane receives the same total. The tree is fixed
-// (pairs 1, 2, then half-row and row mirrors, then rows 16 and 32 apart), and IEEE addition is
-// commutative, so a value's sum never depends on which lane asks or on how many values the
-// caller reduces.
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Sum over the 64 lanes of a wave (called with the whole wave active); every lane receives the
+// same total. The tree is fixed: pairs 1, 2, then half-row and row mirrors leave every lane of a
+// 16-lane row holding that row's sum; the four row sums r0..r3 (read from lanes 0, 16, 32, 48, no
+// LDS round trip) combine as (r0 + r1) + (r2 + r3). IEEE addition is commutative, so a value's
+// sum never depends on which lane asks or on how many values the caller reduces.
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp<0x141>(v);  // row_half_mirror
   v += dpp<0x140>(v);  // row_mirror
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
-  return v;
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -80,9 +83,7 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<0x4E>(v));
   v = fmaxf(v, dpp<0x141>(v));
   v = fmaxf(v, dpp<0x140>(v));
-  v = fmaxf(v, __shfl_xor(v, 16, kWave));
-  v = fmaxf(v, __shfl_xor(v, 32, kWave));
-  return v;
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
 // Four int8 weights (one 32-bit word, k order) as two exact fp16 pairs. Each byte, offset by

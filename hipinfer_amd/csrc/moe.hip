@@ -36,8 +36,7 @@ constexpr int kGrpBM = 64, kGrpBN = 128;  // grouped GEMM tile (gemm config kGem
 // (reference argmax_better, kernels.cuh:1886-1890).
 __device__ __forceinline__ bool argmax_better(float v, int i, float best, int bi) {
   const bool vn = v != v, bn = best != best;
-  if (vn != bn) return vn;
-  return (vn || v == best) ? i < bi : v > best;
+  return (vn != bn) ? vn : ((vn | (v == best)) ? i < bi : v > best);  // selects, no branches
 }
 
 // ------------------------------------------------------------------ router
@@ -48,8 +47,9 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float best, int bi
 //    memory round trip; every expert's dot product runs in the same order whatever the number of
 //    waves; rounded to fp16 (the router linear's output dtype);
 //  * top k by rank: argmax_better is a strict total order on (logit, index), so the expert that
-//    exactly j others beat is the j-th pick of the sequential argmax, and every expert's rank is
-//    counted in parallel from the logits in LDS;
+//    exactly j others beat is the j-th pick of the sequential argmax; every expert's rank is
+//    counted in parallel (rank_key turns the order into an unsigned compare, one ballot counts 64
+//    rivals);
 //  * weights: softmax over the k (norm_topk) or over all E, rounded to fp16 when the model rounds.
 constexpr int kRouterWaves = 16;
 template <int CH>
@@ -91,16 +91,45 @@ __device__ __forceinline__ void router_logits(const f16* __restrict__ xr, const 
   }
 }
 
-__device__ __forceinline__ void router_topk(const float* logit, int E, int k, int tid, int nthreads, float* selv,
-                                            int* seli) {
-  for (int e = tid; e < E; e += nthreads) {
-    const float v = logit[e];
+// Sort key of (logit v, expert i) in argmax_better's order: NaN above every number, -0 equal to +0,
+// numbers by value (sign-magnitude bits mapped to an increasing unsigned), equal values to the lower
+// index (the low word falls as i rises). Expert o beats expert e exactly when key(o) > key(e).
+__device__ __forceinline__ uint64_t rank_key(float v, int i) {
+  uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  if (v != v) u = 0xFFFFFFFFu;
+  return ((uint64_t)u << 32) | (0xFFFFFFFFu - (uint32_t)i);
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l), hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Every wave of the block calls this with all 64 lanes: lane l holds the keys of experts l, l + 64,
+// ...; wave w ranks experts w, w + nwaves, ... with one ballot per 64 candidates.
+__device__ __forceinline__ void router_topk(const float* logit, int E, int k, int nwaves, int wave, int lane,
+                                            float* selv, int* seli) {
+  constexpr int C = kMoeMaxE / 64;
+  uint64_t key[C];
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+    const int o = c * 64 + lane;
+    key[c] = o < E ? rank_key(logit[o], o) : 0ull;  // 0 beats nothing
+  }
+  for (int e = wave; e < E; e += nwaves) {
+    const int ce = e >> 6, le = e & 63;
+    uint64_t ke = 0;
+#pragma unroll
+    for (int c = 0; c < C; c++)
+      if (c == ce) ke = readlane_u64(key[c], le);
     int r = 0;
-#pragma unroll 8
-    for (int o = 0; o < E; o++) r += argmax_better(logit[o], o, v, e);
-    if (r < k) {
+#pragma unroll
+    for (int c = 0; c < C; c++)
+      if (c * 64 < E) r += __popcll(__ballot(key[c] > ke));
+    if (r < k && lane == 0) {
       seli[r] = e;
-      selv[r] = v;
+      selv[r] = logit[e];
     }
   }
 }
@@ -110,16 +139,17 @@ __device__ __forceinline__ void router_weights(const float* logit, const float* 
                                                int flags, int lane, int t, int* __restrict__ idx_out,
                                                float* __restrict__ w_out) {
   const float mx = selv[0];
+  const float ej = lane < k ? expf(selv[lane] - mx) : 0.f;  // lane j: slot j's exponential
   float denom = 0.f;
   if (flags & kMoeNormTopk) {
-    for (int j = 0; j < k; j++) denom += expf(selv[j] - mx);
+    for (int j = 0; j < k; j++) denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ej), j));  // slot order
   } else {
     float sum = 0.f;
     for (int e = lane; e < E; e += 64) sum += expf(logit[e] - mx);
     denom = wave_sum(sum);
   }
   if (lane < k) {
-    float wj = expf(selv[lane] - mx) / denom;
+    float wj = ej / denom;
     if (flags & kMoeFp16Weights) wj = (float)(f16)wj;
     idx_out[(int64_t)t * k + lane] = seli[lane];
     w_out[(int64_t)t * k + lane] = wj;
@@ -138,7 +168,7 @@ __global__ void __launch_bounds__(kRouterWaves * 64) moe_router_kernel(const f16
   const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   router_logits<CH>(xn + t * ldx, Wr, E, H, kRouterWaves, wave, lane, logit);
   __syncthreads();
-  router_topk(logit, E, k, threadIdx.x, kRouterWaves * 64, selv, seli);
+  router_topk(logit, E, k, kRouterWaves, wave, lane, selv, seli);
   __syncthreads();
   if (wave == 0) router_weights(logit, selv, seli, E, k, flags, lane, t, idx_out, w_out);
 }
@@ -219,7 +249,7 @@ __global__ void __launch_bounds__(kFusedWaves * 64) moe_route_gu_kernel(const f1
   const f16* xr = xn + (int64_t)t * ldx;
   router_logits<CH>(xr, Wr, E, H, kFusedWaves, wave, lane, logit);
   __syncthreads();
-  router_topk(logit, E, k, threadIdx.x, kFusedWaves * 64, selv, seli);
+  router_topk(logit, E, k, kFusedWaves, wave, lane, selv, seli);
   __syncthreads();
   if (j == 0 && w0 == (int64_t)p * I && wave == 0) router_weights(logit, selv, seli, E, k, flags, lane, t, idx_out, w_out);
   const int64_t w = w0 + wave;
@@ -442,14 +472,19 @@ size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 // The largest row count the GEMV path takes: HIPINFER_GEMV_MAX, shared with the decode step.
 int gemv_max() { return hi_gemv_max_rows(); }
 
-// The expert workspace (hi_moe_work_bytes), each piece on a 256-byte boundary.
+// The expert workspace (hi_moe_work_bytes), each piece on a 256-byte boundary. The first
+// kMoeBarBytes (at a fixed offset, whatever M) hold the one-token launch's arrival counters.
+constexpr int kMoeBarStride = 64;                 // words between two arrival counters (256 bytes)
+constexpr size_t kMoeBarBytes = 9 * 256;          // 8 counters, then the 8 expected totals
 struct MoeWork {
+  unsigned* bar;
   int *perm, *inv, *off, *tiles;
   f16 *rows, *y, *act;
 };
 MoeWork moe_work(void* work, int n, int E, int H) {
   char* p = (char*)work;
   MoeWork m;
+  m.bar = (unsigned*)p; p += kMoeBarBytes;
   m.perm = (int*)p;   p += al256((size_t)n * 4);
   m.inv = (int*)p;    p += al256((size_t)n * 4);
   m.off = (int*)p;    p += al256((size_t)(E + 1) * 4);
@@ -469,6 +504,262 @@ int moe_down_launch(const f16* act, const f16* Wd, const int* idx, const float* 
                      Wd, idx, w, M, k, E, H, I, flags, scale, (f16*)x, (int64_t)ldx);
   HI_TRY(hipGetLastError());
   return 0;
+}
+
+
+// ------------------------------------------------------------------ one-launch decode (one token)
+// Router, gate/up + SwiGLU, down projection, weighted combine and residual for ONE token in a single
+// launch whose blocks are all resident at once (the host checks the occupancy). Phase 1 is
+// moe_route_gu_kernel's work (same device functions, same bits). The activations go out with
+// agent-coherent stores; a grid handoff (arrival counters, relaxed agent-scope atomics, no L2
+// writeback fence) separates the phases. Once a block has arrived, the waves that own its
+// down-projection columns issue their k expert rows' loads, so those weights stream while the grid
+// waits. Phase 2 copies the token's activations into LDS once per block with agent-coherent 16-byte
+// loads and runs moe_gemv_down_kernel's arithmetic, one wave per hidden column.
+// The handoff counts arrivals on eight counters in the caller's work buffer (block b on counter
+// b % 8, 256 bytes apart so they sit in different memory channels) that are never reset: the
+// word after them, expect[x], holds what counter x reads once every launch so far has arrived, so
+// a launch's target is that plus its own arrivals on x. Each block adds 1 (no returned value) once
+// its activations are complete; one wave per block polls the eight counters (one load each per
+// poll); block 0 then advances expect (every block has read it by then: a block reads it before it
+// arrives). A zeroed region is consistent (0 == 0) and every launch leaves it consistent; calls that
+// share a work buffer must not overlap in time (they share its activations too), calls with their
+// own buffers are independent.
+constexpr int kMoeOneMaxBlocks = 512;  // 16-wave blocks resident at once: at most 2 per CU, 256 CUs
+constexpr int kMoeSpinMax = 1 << 18;  // polls before a block gives up waiting (never reached when resident)
+constexpr int kMoeOneMaxAct = kMoeOneMaxBlocks * 16;  // k * I = 16 units per block
+constexpr int kMoeRawBuffer = 0x00020000;  // buffer resource word 3: raw (untyped) 32-bit access
+constexpr int kMoeSc1 = 16;                // buffer cache policy sc1: agent-coherent, as an agent-scope load
+
+__device__ __forceinline__ uint32_t ld_coherent_u32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int CH, int KM, int RND>
+__global__ void __launch_bounds__(kFusedWaves * 64) moe_decode_one_kernel(
+    const f16* __restrict__ xn, const f16* __restrict__ Wr, const f16* __restrict__ wgu,
+    const f16* __restrict__ wdown, int k, int E, int H, int I, int flags, float scale, int cols_per_block,
+    int* __restrict__ idx_out, float* __restrict__ w_out, uint32_t* act2, f16* x, unsigned* bar) {
+  __shared__ float logit[kMoeMaxE];
+  __shared__ float selv[kMoeMaxK];
+  __shared__ int seli[kMoeMaxK];
+  __shared__ f16 unit_out[kFusedWaves];
+  __shared__ int ridx[kMoeMaxK];
+  __shared__ float rw[kMoeMaxK];
+  __shared__ u32x4 act_s[kMoeOneMaxAct / 8];  // the token's k * I activations, 8 halves a word
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nb = gridDim.x;
+  constexpr int kPoller = kFusedWaves - 1;  // the wave that arrives and polls (a down wave only when
+                                            // every wave is one)
+  // lane x < 8 of the poller: counter x's target (needed only at the handoff, so the load's latency
+  // is hidden)
+  const unsigned target =
+      (wave == kPoller && lane < 8) ? ld_coherent_u32(&bar[8 * kMoeBarStride + lane]) + (unsigned)((nb - lane + 7) / 8) : 0u;
+  // this block's down-projection column (one per wave) and its residual, read early: no other block
+  // writes it
+  const int h = blockIdx.x * cols_per_block + wave;
+  const bool down_wave = wave < cols_per_block && h < H;
+  f16 xh = (f16)0.f;
+  if (down_wave && lane == 0) xh = x[h];
+  // ---- phase 1a: the routing (every block computes the token's own, as moe_route_gu_kernel)
+  router_logits<CH>(xn, Wr, E, H, kFusedWaves, wave, lane, logit);
+  __syncthreads();
+  router_topk(logit, E, k, kFusedWaves, wave, lane, selv, seli);
+  __syncthreads();
+  // every block forms the weights itself (into LDS; block 0 also writes them out), so phase 2 never
+  // reads another block's plain stores
+  if (wave == 0) {
+    router_weights(logit, selv, seli, E, k, flags, lane, 0, ridx, rw);
+    if (blockIdx.x == 0) router_weights(logit, selv, seli, E, k, flags, lane, 0, idx_out, w_out);
+  }
+  // ---- phase 1b: gate/up + SwiGLU of this block's 16 units (pair p = slot j, units o0 .. o0 + 15)
+  {
+    const int64_t w0 = (int64_t)blockIdx.x * kFusedWaves;
+    const int j = (int)(w0 / I);
+    const int o = (int)(w0 - (int64_t)j * I) + wave;
+    const int e = seli[j];
+    const int r0 = (o >> 4) * 32 + (o & 15);
+    const f16* g = wgu + ((int64_t)e * 2 * I + r0) * H;
+    const f16* u = g + 16 * (int64_t)H;
+    const int H8 = H / 8;
+    float ag = 0.f, au = 0.f;
+    for (int b = 0; b < H8; b += 64 * CH) {
+      u32x4 xv[CH], gv[CH], uv[CH];
+#pragma unroll
+      for (int q = 0; q < CH; q++) {
+        const int c = b + q * 64 + lane, cc = c < H8 ? c : 0;
+        xv[q] = *reinterpret_cast<const u32x4*>(xn + 8 * cc);
+        gv[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g + 8 * cc));
+        uv[q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(u + 8 * cc));
+      }
+#pragma unroll
+      for (int q = 0; q < CH; q++) {
+        const bool ok = b + q * 64 + lane < H8;
+#pragma unroll
+        for (int hh = 0; hh < 4; hh++) {
+          const f16x2 x2 = as_h2(ok ? xv[q][hh] : 0u);
+          ag = dot2(as_h2(gv[q][hh]), x2, ag);
+          au = dot2(as_h2(uv[q][hh]), x2, au);
+        }
+      }
+    }
+    ag = wave_sum(ag);
+    au = wave_sum(au);
+    if (lane == 0) unit_out[wave] = silu_mul(ag, au);
+    __syncthreads();
+    // the block's 16 units leave as 8 agent-coherent words of fp16 pairs
+    if (tid < kFusedWaves / 2) {
+      const uint32_t pair = as_u32(f16x2{unit_out[2 * tid], unit_out[2 * tid + 1]});
+      __hip_atomic_store(act2 + ((int64_t)j * I + (o - wave)) / 2 + tid, pair, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // ---- grid handoff: the activation words are complete before this block arrives
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  if (wave == kPoller && lane == 0)
+    __hip_atomic_fetch_add(&bar[(blockIdx.x & 7) * kMoeBarStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the down waves' weight rows (all k experts of the block's columns) stream during the handoff
+  const int I8 = I / 8;  // I <= 64 * 8 * RND (the host's choice of RND)
+  u32x4 wv[KM][RND];
+#pragma unroll
+  for (int j = 0; j < KM; j++)
+#pragma unroll
+    for (int rr = 0; rr < RND; rr++) wv[j][rr] = u32x4{0u, 0u, 0u, 0u};
+  if (down_wave) {
+#pragma unroll
+    for (int j = 0; j < KM; j++) {
+      if (j < k) {
+        const int e = seli[j];
+#pragma unroll
+        for (int rr = 0; rr < RND; rr++) {
+          const int c = rr * 64 + lane;
+          if (c < I8)
+            wv[j][rr] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wdown + ((int64_t)e * H + h) * I + 8 * c));
+        }
+      }
+    }
+  }
+  // every block waits for every arrival (all blocks are resident, so every wait ends; the poll
+  // count is bounded all the same)
+  if (wave == kPoller) {
+    // one poll in flight: a second one (checked while the next is out) measured slower, the
+    // counters' memory channel serving the polls and the arrivals alike
+    for (int it = 0; it < kMoeSpinMax; it++) {
+      const bool ok = lane >= 8 || (int)(ld_coherent_u32(&bar[lane * kMoeBarStride]) - target) >= 0;
+      if (__all(ok)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (blockIdx.x == 0 && lane < 8) __hip_atomic_store(&bar[8 * kMoeBarStride + lane], target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  // ---- phase 2: the activations into LDS once per block (agent-coherent 16-byte loads), then the
+  //      down projection + weighted combine (slot order) + residual, one wave per column
+  {
+    const int n16 = k * I / 8;
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(act2, (short)0, n16 * 16, kMoeRawBuffer);
+    for (int i = tid; i < n16; i += kFusedWaves * 64) act_s[i] = __builtin_amdgcn_raw_buffer_load_b128(ar, i * 16, 0, kMoeSc1);
+  }
+  __syncthreads();
+  if (down_wave) {
+    float acc[KM];
+#pragma unroll
+    for (int j = 0; j < KM; j++) acc[j] = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < RND; rr++) {
+      const int c = rr * 64 + lane;
+      if (rr * 64 < I8) {  // uniform over the wave
+#pragma unroll
+        for (int j = 0; j < KM; j++) {
+          if (j < k) {
+            const u32x4 av = c < I8 ? act_s[j * I8 + c] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int q = 0; q < 4; q++) acc[j] = dot2(as_h2(wv[j][rr][q]), as_h2(av[q]), acc[j]);
+          }
+        }
+      }
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < KM; j++) {
+      if (j < k) {
+        float c = (float)(f16)wave_sum(acc[j]) * rw[j];
+        asm volatile("" : "+v"(c));  // the fp32 product is what gets rounded to fp16
+        sum += (flags & kMoeFp16Weights) ? (float)(f16)c : c;
+      }
+    }
+    if (lane == 0) {
+      f16 o = (f16)sum;
+      if (scale != 1.f) {
+        float t = (float)o * scale;
+        asm volatile("" : "+v"(t));  // fp32 product, then fp16 (two roundings)
+        o = (f16)t;
+      }
+      x[h] = xh + o;
+    }
+  }
+}
+
+// Launches moe_decode_one_kernel for one token when its grid can be resident all at once: k * I / 16
+// blocks of 16 waves (each 16 gate/up units, then up to 16 down columns). Returns 0 after the
+// launch, 1 when the shape or the occupancy does not allow it (the caller takes the two launches),
+// or a negative error code.
+template <int CH, int KM, int RND>
+int moe_decode_one_go(const void* xn, const void* Wr, const void* wgu, const void* wdown, int E, int k, int H, int I,
+                      int flags, float scale, void* x, int* idx, float* w, void* act, unsigned* bar, int nb, int cpb,
+                      hipStream_t st) {
+  const HiDevice* d = hi_device();
+  if (!d) return -2;
+  auto fn = moe_decode_one_kernel<CH, KM, RND>;
+  const int bpc = hi_blocks_per_cu(reinterpret_cast<const void*>(fn), kFusedWaves * 64, 0);
+  if (bpc < 0) return -2;
+  if ((long)bpc * d->cus < nb) return 1;  // not resident at once: the handoff could not be waited for
+  hipLaunchKernelGGL(fn, dim3(nb), dim3(kFusedWaves * 64), 0, st, (const f16*)xn, (const f16*)Wr, (const f16*)wgu,
+                     (const f16*)wdown, k, E, H, I, flags, scale, cpb, idx, w, (uint32_t*)act, (f16*)x, bar);
+  HI_TRY(hipGetLastError());
+  return 0;
+}
+
+template <int CH, int RND>
+int moe_decode_one_k(const void* xn, const void* Wr, const void* wgu, const void* wdown, int E, int k, int H, int I,
+                     int flags, float scale, void* x, int* idx, float* w, void* act, unsigned* bar, int nb, int cpb,
+                     hipStream_t st) {
+  if (k <= 4)
+    return moe_decode_one_go<CH, 4, RND>(xn, Wr, wgu, wdown, E, k, H, I, flags, scale, x, idx, w, act, bar, nb, cpb, st);
+  if (k <= 8 && RND <= 2)
+    return moe_decode_one_go<CH, 8, RND <= 2 ? RND : 2>(xn, Wr, wgu, wdown, E, k, H, I, flags, scale, x, idx, w, act, bar,
+                                                        nb, cpb, st);
+  if (RND == 1)
+    return moe_decode_one_go<CH, 16, 1>(xn, Wr, wgu, wdown, E, k, H, I, flags, scale, x, idx, w, act, bar, nb, cpb, st);
+  return 1;  // k * (I / 512) above 16 rounds of expert rows per lane: more registers than this kernel holds
+}
+
+// HIPINFER_MOE_ONE_LAUNCH=0 turns the one-launch path off (read once): its handoff needs every block
+// resident at once, which other kernels running concurrently on the GPU could prevent.
+bool moe_one_launch_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("HIPINFER_MOE_ONE_LAUNCH");
+    return !e || atoi(e) != 0;
+  }();
+  return on;
+}
+
+int moe_decode_one(const void* xn, const void* Wr, const void* wgu, const void* wdown, int E, int k, int H, int I,
+                   int flags, float scale, void* x, int* idx, float* w, void* act, unsigned* bar, hipStream_t st) {
+  if (!moe_one_launch_enabled()) return 1;
+  if ((int64_t)k * I % kFusedWaves || I > 2048) return 1;
+  const int nb = k * I / kFusedWaves;
+  if (nb > kMoeOneMaxBlocks) return 1;
+  const int cpb = (H + nb - 1) / nb;
+  if (cpb > kFusedWaves) return 1;
+  const int rnd = I <= 512 ? 1 : I <= 1024 ? 2 : 4;
+  const int ch = chunks_for(H);
+#define HI_MOE_ONE(C, R)   \
+  if (ch == C && rnd == R) \
+    return moe_decode_one_k<C, R>(xn, Wr, wgu, wdown, E, k, H, I, flags, scale, x, idx, w, act, bar, nb, cpb, st);
+  HI_MOE_ONE(1, 1) HI_MOE_ONE(1, 2) HI_MOE_ONE(1, 4) HI_MOE_ONE(2, 1) HI_MOE_ONE(2, 2) HI_MOE_ONE(2, 4)
+  HI_MOE_ONE(4, 1) HI_MOE_ONE(4, 2) HI_MOE_ONE(4, 4)
+#undef HI_MOE_ONE
+  return 1;
 }
 
 }  // namespace
@@ -491,11 +782,12 @@ HI_EXPORT int hi_moe_router(const void* xn, int ldx, const void* Wr, int M, int 
   return 0;
 }
 
-// Expert workspace, each piece on a 256-byte boundary: perm, inv [M*k] int, off, tiles [E+1] int,
-// rows [M*k, H], y [M*k, H] and act [M*k, I] fp16. The GEMV path uses only act.
+// Expert workspace, each piece on a 256-byte boundary: the one-token launch's arrival counters
+// (2304 bytes, first, whatever M), perm, inv [M*k] int, off, tiles [E+1] int, rows [M*k, H],
+// y [M*k, H] and act [M*k, I] fp16. The GEMV path uses only act.
 HI_EXPORT size_t hi_moe_work_bytes(int M, int k, int E, int H, int I) {
   const size_t n = (size_t)(M > 0 ? M : 0) * (k > 0 ? k : 0);
-  return 2 * al256(n * 4) + 2 * al256((size_t)(E + 1) * 4) + 2 * al256(n * H * 2) + al256(n * I * 2);
+  return kMoeBarBytes + 2 * al256(n * 4) + 2 * al256((size_t)(E + 1) * 4) + 2 * al256(n * H * 2) + al256(n * I * 2);
 }
 
 // x[m] += MoE(xn[m]) for M rows given the routing (idx, w from hi_moe_router): wgu [E][2I, H]
@@ -551,10 +843,13 @@ HI_EXPORT int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const vo
 
 // Router and experts in one call: x[m] += MoE(xn[m]) for M rows, with the routing computed here and
 // written to idx / w as hi_moe_router writes it. The same bits as hi_moe_router followed by
-// hi_moe_experts with path 0. On the GEMV path (M <= HIPINFER_GEMV_MAX) the router runs inside
+// hi_moe_experts with path 0. One row runs as one launch (moe_decode_one_kernel) when its grid fits
+// on the GPU at once; otherwise, on the GEMV path (M <= HIPINFER_GEMV_MAX), the router runs inside
 // the gate/up launch (moe_route_gu_kernel), which saves a launch and a dependent memory round trip
-// per layer; larger M run the router and the grouped experts as two calls. No counterpart in the
-// reference, whose engine makes the two calls (api.cu:1701-1703); this build's engine uses this.
+// per layer; larger M run the router and the grouped experts as two calls. The work buffer must be
+// zeroed once before its first use here (its arrival counters; every call leaves them consistent).
+// No counterpart in the reference, whose engine makes the two calls (api.cu:1701-1703); this
+// build's engine uses this.
 HI_EXPORT int hi_moe_route_experts(const void* xn, int ldxn, const void* Wr, const void* wgu, const void* wdown, int M,
                                    int E, int k, int H, int I, int flags, float scale, void* x, int ldx, int* idx,
                                    float* w, void* work, void* s) {
@@ -576,6 +871,10 @@ HI_EXPORT int hi_moe_route_experts(const void* xn, int ldxn, const void* Wr, con
   const hipStream_t st = (hipStream_t)s;
   const int n = M * k;
   const MoeWork wk = moe_work(work, n, E, H);
+  if (M == 1) {
+    const int r = moe_decode_one(xn, Wr, wgu, wdown, E, k, H, I, flags, scale, x, idx, w, wk.act, wk.bar, st);
+    if (r <= 0) return r;  // launched (0) or failed (< 0); 1: this shape takes the two launches
+  }
   const int64_t gu_waves = (int64_t)n * I;
   const auto gu = chunks_for(H) == 1 ? moe_route_gu_kernel<1> : chunks_for(H) == 2 ? moe_route_gu_kernel<2>
                                                                                   : moe_route_gu_kernel<4>;

@@ -258,8 +258,11 @@ def _routing(xn, M, k):
             torch.empty(M, k, dtype=torch.float32, device=xn.device))
 
 
-def _moe_work(xn, M, k, E, H, I):
-    return torch.empty(lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device=xn.device)
+def _moe_work(xn, M, k, E, H, I, zeroed=False):
+    """The expert work buffer; moe_route_experts needs it zeroed (its first 2304 bytes are arrival
+    counters that must start consistent)."""
+    make = torch.zeros if zeroed else torch.empty
+    return make(lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device=xn.device)
 
 
 def moe_router(xn, Wr, k, flags):
@@ -290,15 +293,16 @@ def moe_experts(xn, wgu, wdown, idx, w, x, flags, scale=1.0, path=0):
 
 
 def moe_route_experts(xn, Wr, wgu, wdown, k, x, flags, scale=1.0):
-    """moe_router followed by moe_experts(path=0) as one library call with the same results; on the
-    GEMV path (up to HIPINFER_GEMV_MAX rows) the routing runs inside the gate/up launch. Returns the
-    routing (idx, weights)."""
+    """moe_router followed by moe_experts(path=0) as one library call with the same results: one row
+    runs as a single launch when its grid fits on the GPU at once, else on the GEMV path (up to
+    HIPINFER_GEMV_MAX rows) the routing runs inside the gate/up launch. Returns the routing
+    (idx, weights)."""
     for t in (xn, x):
         _need("moe_route_experts", t, torch.float16, 2, rows=True)
     M, H = xn.shape
     E, I = wgu.shape[0], wdown.shape[2]
     idx, w = _routing(xn, M, k)
-    work = _moe_work(xn, M, k, E, H, I)
+    work = _moe_work(xn, M, k, E, H, I, zeroed=True)
     check_rc(lib.hi_moe_route_experts(ptr(xn), xn.stride(0), ptr(Wr), ptr(wgu), ptr(wdown), M, E, k, H, I, flags,
                                       scale, ptr(x), x.stride(0), ptr(idx), ptr(w), ptr(work), cur_stream()),
              "moe_route_experts")

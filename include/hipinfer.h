@@ -87,10 +87,11 @@ int hi_gemm_noalloc(const void* A, int lda, const void* W, const void* scales, c
  * Replaces api.cu:849-857 (hi_moe_router); hipinfer.py:68. */
 int hi_moe_router(const void* xn, int ldx, const void* Wr, int M, int E, int H, int k, int flags, int* idx, float* w,
                   void* stream);
-/* Bytes of the workspace hi_moe_experts needs. Replaces api.cu:862-865 (hi_moe_work_bytes); hipinfer.py:69. */
+/* Bytes of the workspace hi_moe_experts and hi_moe_route_experts need (the first 2304 bytes hold
+ * hi_moe_route_experts' arrival counters). Replaces api.cu:862-865 (hi_moe_work_bytes); hipinfer.py:69. */
 size_t hi_moe_work_bytes(int M, int k, int E, int H, int I);
 /* x[m] += MoE(xn[m]) given the routing: wgu [E][2I, H] (gate/up interleaved per expert), wdown [E][H, I];
- * scale multiplies the combined output (rounded); path 0 auto (GEMV for M <= HIPINFER_GEMV_MAX, default 4),
+ * scale multiplies the combined output (rounded); path 0 auto (GEMV for M <= HIPINFER_GEMV_MAX, default 8),
  * 1 GEMV, 2 grouped MFMA GEMMs (device-side expert grouping, no host round trip). H % 32 == 0, I % 32 == 0.
  * Replaces api.cu:872-911 (hi_moe_experts); hipinfer.py:71. */
 int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const void* wdown, const int* idx, const float* w, int M,
@@ -98,8 +99,11 @@ int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const void* wdown,
                    void* stream);
 /* Router and experts in one call: x[m] += MoE(xn[m]) with the routing computed here and written to
  * idx[M, k] / w[M, k] as hi_moe_router writes it; the same bits as hi_moe_router followed by
- * hi_moe_experts(path 0). For M <= HIPINFER_GEMV_MAX the router runs inside the gate/up launch (one
- * launch and one dependent memory round trip fewer per layer). work: hi_moe_work_bytes(M, k, E, H, I).
+ * hi_moe_experts(path 0). M = 1 runs as one launch (router, gate/up, a grid-wide handoff, down and
+ * combine) when that grid fits on the GPU at once; otherwise, for M <= HIPINFER_GEMV_MAX, the router
+ * runs inside the gate/up launch. work: hi_moe_work_bytes(M, k, E, H, I), zeroed once before its
+ * first use with this function (the one-launch path keeps arrival counters in it and leaves them
+ * consistent); calls that share a work buffer must not overlap in time.
  * No counterpart in the reference (its engine makes the two calls, api.cu:1701-1703); for callers
  * that run a whole MoE layer, such as this library's engine. */
 int hi_moe_route_experts(const void* xn, int ldxn, const void* Wr, const void* wgu, const void* wdown, int M, int E,

@@ -170,7 +170,7 @@ def test_moe_route_experts_graph_replay(hi):
     x = x0.clone()
     idx = torch.empty(M, k, dtype=torch.int32, device="cuda")
     w = torch.empty(M, k, dtype=torch.float32, device="cuda")
-    work = torch.empty(hi.lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device="cuda")
+    work = torch.zeros(hi.lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device="cuda")
 
     def run():
         hi.check_rc(hi.lib.hi_moe_route_experts(hi.ptr(xn), H, hi.ptr(Wr), hi.ptr(wgu), hi.ptr(wdn), M, E, k, H, I, flags, 0.22,
@@ -189,6 +189,33 @@ def test_moe_route_experts_graph_replay(hi):
         assert np.array_equal(host(x).view(np.uint16), ref.view(np.uint16))
         assert np.array_equal(host(idx), host(idx2))
         hi.moe_route_experts(xn, Wr, wgu, wdn, k, x0.clone(), flags, 0.22)  # eager work between replays
+
+
+def test_moe_route_experts_shared_work_across_shapes(hi):
+    """One zeroed work buffer serves single-row calls of every layer shape in turn, twice round:
+    the one-launch path's arrival counters live in it and carry each launch's totals to the next
+    (grids of 32 to 256 blocks), and every call still equals the two calls bit for bit."""
+    import torch
+    r = rng(460)
+    layers = []
+    for name, E, k, H, I, flags, scale in LAYERS:
+        layers.append((name, E, k, H, I, flags, scale, cuda(rn(r, E, H, s=0.05)), cuda(rn(r, E, 2 * I, H, s=0.02)),
+                       cuda(rn(r, E, H, I, s=0.02))))
+    nbytes = max(hi.lib.hi_moe_work_bytes(1, k, E, H, I) for _, E, k, H, I, *_ in layers)
+    work = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    for rnd in range(2):
+        for name, E, k, H, I, flags, scale, Wr, wgu, wdn in layers:
+            xn, x0 = cuda(rn(r, 1, H)), cuda(rn(r, 1, H))
+            idx2, w2 = hi.moe_router(xn, Wr, k, flags)
+            ref = host(hi.moe_experts(xn, wgu, wdn, idx2, w2, x0.clone(), flags, scale, 0))
+            x = x0.clone()
+            idx = torch.empty(1, k, dtype=torch.int32, device="cuda")
+            w = torch.empty(1, k, dtype=torch.float32, device="cuda")
+            hi.check_rc(hi.lib.hi_moe_route_experts(hi.ptr(xn), H, hi.ptr(Wr), hi.ptr(wgu), hi.ptr(wdn), 1, E, k, H, I,
+                                                    flags, scale, hi.ptr(x), H, hi.ptr(idx), hi.ptr(w), hi.ptr(work),
+                                                    hi.cur_stream()), "moe_route_experts")
+            assert np.array_equal(host(idx), host(idx2)), f"{name} round {rnd}: routing differs"
+            assert np.array_equal(host(x).view(np.uint16), ref.view(np.uint16)), f"{name} round {rnd}: output differs"
 
 
 def test_moe_route_experts_rejects_bad_arguments(hi):
