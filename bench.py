@@ -527,6 +527,9 @@ def _time(torch, fn, steps):
     return ms
 
 
+C4_DIMS = (1536, 12, 2, 128, 8960, 151936)  # Qwen2.5-1.5B: hidden, q heads, kv heads, head dim, MLP, vocab
+
+
 def decode_config_bench(torch, hi, name, dims, M_list, n_layers, steps, seed, q8_too=True, bias=False):
     """A model's decode GEMV set (QKV+RoPE, o + residual, gate/up + SwiGLU, down + residual per layer,
     then lm_head) over n_layers distinct weight sets, for each row count M: weight GB/s per token."""
@@ -775,7 +778,7 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C4 / C5 sections")
     ap.add_argument("--no-step", action="store_true", help="skip the whole decode step (with attention) section")
     ap.add_argument("--no-engine", action="store_true", help="skip the engine prefill / batched decode section")
-    ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe"] +
+    ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe", "c4"] +
                     [k + q for k in ("qkv", "o", "gate_up", "down", "lm_head") for q in ("", "8")], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
     args = ap.parse_args()
@@ -793,6 +796,10 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)}, {hi.lib.hi_device_cus()} CUs")
     if args.profile == "moe":
         log(json.dumps(moe_bench(torch, hi, args.steps, SEED + 12)))
+        return
+    if args.profile == "c4":  # the C4 GEMV set at 8 rows (speculative-verify width), fp16 then int8
+        log(json.dumps(decode_config_bench(torch, hi, "C4 at 8 rows", C4_DIMS, [8], 28, args.steps, SEED + 11,
+                                           bias=True)))
         return
     t0 = time.perf_counter()
     model = Model(torch, hi, q8_too=not args.no_int8)
@@ -902,7 +909,7 @@ def main():
             "C1_tinyllama": decode_config_bench(torch, hi, "TinyLlama-1.1B decode GEMV set (22 distinct layers)",
                                                 (2048, 32, 4, 64, 5632, 32000), [1], 22, args.steps, SEED + 10),
             "C4_qwen25_1p5b": decode_config_bench(torch, hi, "Qwen2.5-1.5B decode/verify GEMV set with QKV bias "
-                                                  "(28 distinct layers), N rows", (1536, 12, 2, 128, 8960, 151936),
+                                                  "(28 distinct layers), N rows", C4_DIMS,
                                                   [1, 2, 5, 8], 28, args.steps, SEED + 11, bias=True),
             "C5_granite_moe": moe_bench(torch, hi, args.steps, SEED + 12),
         }

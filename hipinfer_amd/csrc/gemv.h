@@ -20,8 +20,9 @@
 //    weights; each lane's sums start at -1152 times the activation elements it meets, so the
 //    offset is never subtracted per weight) and every pair of weights meets its activation pair
 //    in one v_dot2_f32_f16 (fp32 accumulate);
-//  * a fixed DPP/swizzle butterfly reduces each row over the wave; the int8 row scale is applied
-//    once to the reduced sum, then the epilogue runs on lane m for activation row m.
+//  * a fixed DPP/swizzle butterfly reduces each row over the wave (from 4 sums on, all of an
+//    item's rows at once, scattered over the lanes with the same tree); the int8 row scale is
+//    applied once to the reduced sum, then the epilogue runs on lane m for activation row m.
 // A row's arithmetic never depends on M, the unit schedule or the grid: row m of an M-row GEMV is
 // bit-identical to the 1-row GEMV of that row (the reference's promise, api.cu:153-155, that
 // speculative verification relies on).
@@ -77,8 +78,10 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   // lane (32 for 8-byte loads), 128 for the SwiGLU launches and 32 for the int8 residual ones:
   // measured on MI355X, launches whose waves stream several items (gate/up) run fastest on the
   // larger steps, launches of about one item per wave (QKV, o, down) on the smaller ones, which
-  // overlap more of the item's latency (int8 o / down: 5.24 / 11.32 us against 5.31 / 11.39).
-  constexpr int UN = (EPI == 2 ? 8 : (EPI == 1 && WF == WF_I8) ? 2 : 4) * (WF == WF_I8H ? 2 : 1);
+  // overlap more of the item's latency (int8 o / down: 5.24 / 11.32 us against 5.31 / 11.39). From 4
+  // activation rows on, the SwiGLU launches take the smaller step too: it frees the registers for a
+  // second block per CU (C4 gate/up at 8 rows: fp16 13.6 against 14.7 us, int8 14.4 against 14.7).
+  constexpr int UN = (EPI == 2 ? (MR >= 4 ? 4 : 8) : (EPI == 1 && WF == WF_I8) ? 2 : 4) * (WF == WF_I8H ? 2 : 1);
   constexpr int U = UN / R > 0 ? UN / R : 1;
   constexpr int SW = 64 * U;                            // chunks of a row per step
   constexpr int XC = MR <= 8 ? (MR <= 4 ? 4 / MR : 1) : 0;  // activation chunks per row held in registers
@@ -87,6 +90,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   constexpr bool BIAS = WF != WF_F16;                    // int8 weights unpacked with an offset (below)
   extern __shared__ u32x4 xs[];                         // [MR][K / 8] activation chunks
   __shared__ float red[kGemvWaves][MR];
+  __shared__ float rinv[MR];
   __shared__ float xp[BIAS ? MR : 1][BIAS ? kGemvThreads : 1];  // per staging thread: its chunks' sum
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -229,21 +233,29 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
             }
           }
     }
+    if constexpr (MR >= 4) {  // one scattered reduction: lane m ends with row m's sum
+      wave_sum_scatter<MR>(ss, lane);
+      if (lane < MR) red[wave][lane] = ss[0];
+    } else {
 #pragma unroll
-    for (int m = 0; m < MR; m++) ss[m] = wave_sum(ss[m]);
-    if (lane == 0) {
+      for (int m = 0; m < MR; m++) ss[m] = wave_sum(ss[m]);
+      if (lane == 0) {
 #pragma unroll
-      for (int m = 0; m < MR; m++) red[wave][m] = ss[m];
+        for (int m = 0; m < MR; m++) red[wave][m] = ss[m];
+      }
+    }
+    __syncthreads();
+    // row m's inverse RMS, formed once (thread m) and read by every thread
+    if (tid < MR) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < kGemvWaves; w++) tot += red[w][tid];
+      rinv[tid] = 1.0f / __builtin_sqrtf(tot / (float)K + a.eps);
     }
     __syncthreads();
     float r[MR];
 #pragma unroll
-    for (int m = 0; m < MR; m++) {
-      float tot = 0.f;
-#pragma unroll
-      for (int w = 0; w < kGemvWaves; w++) tot += red[w][m];
-      r[m] = 1.0f / __builtin_sqrtf(tot / (float)K + a.eps);
-    }
+    for (int m = 0; m < MR; m++) r[m] = rinv[m];
     auto norm_chunk = [&](u32x4 v, u32x4 wv_, float rm) {
       u32x4 o;
 #pragma unroll
@@ -285,10 +297,28 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
         }
       }
     } else {
-      for (int c = tid; c < K8; c += kGemvThreads)
+      // SB chunks of every row per thread are loaded together before any is stored, so a long
+      // row costs about one memory round trip, not one per chunk (a row's chunks are still put in
+      // increasing order)
+      constexpr int SB = MR >= 16 ? 2 : 4;
+      for (int c0 = tid; c0 < K8; c0 += SB * kGemvThreads) {
+        u32x4 v[SB][MR];
 #pragma unroll
-        for (int m = 0; m < MR; m++)
-          put(m, c, m < M ? *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c) : u32x4{0u, 0u, 0u, 0u});
+        for (int i = 0; i < SB; i++) {
+          const int c = c0 + i * kGemvThreads;
+#pragma unroll
+          for (int m = 0; m < MR; m++)
+            v[i][m] = (c < K8 && m < M) ? *reinterpret_cast<const u32x4*>(a.x + m * a.ldx + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < SB; i++) {
+          const int c = c0 + i * kGemvThreads;
+          if (c < K8) {
+#pragma unroll
+            for (int m = 0; m < MR; m++) put(m, c, v[i][m]);
+          }
+        }
+      }
     }
   }
   if constexpr (BIAS) {
@@ -391,20 +421,44 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
     for (int g = 0; g < G; g++) y[g] = y2[g] = (f16)0.f;
     const bool last = s == SPI - 1;
     if (last) {
+      // the R x MR sums over the wave (wave_sum's tree), then each lane's row: from 4 sums on, one
+      // scattered reduction of all of them (accumulator j * MR + m ends in lanes l with
+      // l % L == (j * MR + m) % L, slot (j * MR) / L) and a lane read per sum the epilogue needs
+      constexpr int NA = R * MR, L = NA < 16 ? NA : 16;
+      float av0[G], av1[G];
+      if constexpr (NA >= 4) {
+        float v[NA];
 #pragma unroll
-      for (int j = 0; j < R; j++)
+        for (int j = 0; j < R; j++)
 #pragma unroll
-        for (int m = 0; m < MR; m++) acc[j][m] = wave_sum(acc[j][m]);
+          for (int m = 0; m < MR; m++) v[j * MR + m] = acc[j][m];
+        wave_sum_scatter<NA>(v, lane);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+          const int j0 = g * NR * MR, j1 = (g * NR + NR - 1) * MR;
+          av0[g] = __shfl(v[j0 / L], (j0 + lm) % L, kWave);
+          av1[g] = NR == 2 ? __shfl(v[j1 / L], (j1 + lm) % L, kWave) : av0[g];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < R; j++)
+#pragma unroll
+          for (int m = 0; m < MR; m++) acc[j][m] = wave_sum(acc[j][m]);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+          av0[g] = av1[g] = 0.f;  // this lane's row, selected without dynamic register indexing
+#pragma unroll
+          for (int m = 0; m < MR; m++)
+            if (m == lm) {
+              av0[g] = acc[g * NR][m];
+              av1[g] = acc[g * NR + NR - 1][m];
+            }
+        }
+      }
 #pragma unroll
       for (int g = 0; g < G; g++) {
         const int u = t * G + g;
-        float a0 = 0.f, a1 = 0.f;  // this lane's row, selected without dynamic register indexing
-#pragma unroll
-        for (int m = 0; m < MR; m++)
-          if (m == lm) {
-            a0 = acc[g * NR][m];
-            a1 = acc[g * NR + NR - 1][m];
-          }
+        float a0 = av0[g], a1 = av1[g];
         if constexpr (WF != WF_F16) {
           a0 *= (float)pc[g].s0;  // the row scale applied once to the reduced sum (reference kernels.cuh:261)
           a1 *= (float)pc[g].s1;

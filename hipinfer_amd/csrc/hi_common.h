@@ -78,6 +78,64 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
+// DPP row_ror:N (rotate right: data moves to higher lanes) into the lanes of the banks (groups of 4
+// lanes of a 16-lane row) in BANKS; the other lanes return old. Lane l reads lane
+// (l & ~15) | ((l - N) & 15).
+template <int N, int BANKS>
+__device__ __forceinline__ float dpp_ror(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                               0x120 + N, 0xF, BANKS, false));
+}
+
+// The partner value of butterfly stage S: lanes 1, 2, 4 and 8 apart within a row (for 4: lanes 4-7
+// and 12-15 read 4 lanes down, lanes 0-3 and 8-11 read 4 lanes up, a rotate by 12).
+template <int S>
+__device__ __forceinline__ float stage_partner(float v) {
+  if constexpr (S == 0) return dpp<0xB1>(v);  // quad_perm [1,0,3,2]
+  else if constexpr (S == 1) return dpp<0x4E>(v);  // quad_perm [2,3,0,1]
+  else if constexpr (S == 2) return dpp_ror<12, 0x5>(dpp_ror<4, 0xA>(0.f, v), v);
+  else return dpp_ror<8, 0xF>(0.f, v);
+}
+
+template <int S, int NA>
+__device__ __forceinline__ void scatter_stage(float (&v)[NA], int n, int lane) {
+  const bool b = (lane >> S) & 1;
+#pragma unroll
+  for (int k = 0; k < NA / 2; k++)
+    if (2 * k < n) {
+      const float x = v[2 * k], y = v[2 * k + 1];
+      v[k] = (b ? y : x) + stage_partner<S>(b ? x : y);
+    }
+}
+
+// wave_sum of NA accumulators at once (NA a power of 2, called with the whole wave active). The
+// tree is wave_sum's: within a row, the partners 1, 2, 4 and 8 lanes apart (a partner in the other
+// quad or half-row holds the same partial as wave_sum's mirrored one), then the rows 16 and 32
+// apart, (r0 + r1) + (r2 + r3). It is scattered: at stage s < log2(NA) (at most 4) a lane keeps the
+// accumulators whose index bit s equals its lane bit s, adds its partner's partials of those and
+// hands over the others, so each stage does half the adds of the one before. Every total has
+// exactly wave_sum's bits (IEEE addition is commutative). On return, with L = min(NA, 16),
+// v[k] (k < NA / L) of every lane l holds the total of accumulator k * L + (l % L).
+template <int NA>
+__device__ __forceinline__ void wave_sum_scatter(float (&v)[NA], int lane) {
+  constexpr int S = NA >= 16 ? 4 : NA >= 8 ? 3 : NA >= 4 ? 2 : NA >= 2 ? 1 : 0;
+  if constexpr (S > 0) scatter_stage<0>(v, NA, lane);
+  if constexpr (S > 1) scatter_stage<1>(v, NA / 2, lane);
+  if constexpr (S > 2) scatter_stage<2>(v, NA / 4, lane);
+  if constexpr (S > 3) scatter_stage<3>(v, NA / 8, lane);
+  // the stages left over when NA < 16 act on the one value each lane holds
+  if constexpr (S < 1) v[0] += stage_partner<0>(v[0]);
+  if constexpr (S < 2) v[0] += stage_partner<1>(v[0]);
+  if constexpr (S < 3) v[0] += stage_partner<2>(v[0]);
+  if constexpr (S < 4) v[0] += stage_partner<3>(v[0]);
+  constexpr int K = NA > 16 ? NA / 16 : 1;
+#pragma unroll
+  for (int k = 0; k < K; k++) {
+    v[k] += __shfl_xor(v[k], 16, kWave);
+    v[k] += __shfl_xor(v[k], 32, kWave);
+  }
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<0xB1>(v));
   v = fmaxf(v, dpp<0x4E>(v));
