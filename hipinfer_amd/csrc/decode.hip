@@ -9,15 +9,14 @@
 //    head, so the cache is read once per GQA group. A split covers a contiguous run of keys; the
 //    number of splits in use is derived on the device from pos[b], so a captured graph stays valid
 //    while the context grows;
-//  * a wave takes 64-key tiles: the tile's K and V rows go straight into LDS (1 KB per DMA
-//    instruction, all of them in flight at once, the wave's first tile before anything else), so a
-//    tile costs one memory round trip; lane l then owns key t0 + l, reads its K row from LDS and
-//    computes the key's logit for every query head in fp32 with the query chunks in scalar
-//    registers (scalar loads, the same for every lane; q pre-scaled by log2(e) / sqrt(D), the
-//    reference's log2-domain softmax, kernels.cuh:1522);
+//  * a wave takes 64-key tiles: the tile's K rows go straight into LDS (1 KB per DMA instruction)
+//    and its V rows into registers, all in flight at once (the wave's first tile before anything
+//    else), so a tile costs one memory round trip; lane l then owns key t0 + l, reads its K row
+//    from LDS and computes the key's logit for every query head in fp32 with the query chunks in
+//    scalar registers (scalar loads, the same for every lane; q pre-scaled by log2(e) / sqrt(D),
+//    the reference's log2-domain softmax, kernels.cuh:1522);
 //  * online softmax per wave (max and sum over the 64 lanes), P.V with each lane owning D / 64
-//    output dims, the weights as fp16 key pairs through LDS and V read from LDS, the 4 waves
-//    merged through LDS;
+//    output dims and the weights as fp16 key pairs through LDS, the 4 waves merged through LDS;
 //  * splits hand their partials (o, m, l) to the last-arriving block of their (sequence, kv head)
 //    with agent-coherent (sc1) stores and loads and a relaxed agent-scope counter, which the last
 //    block resets: no L2 writeback/invalidate fence (gfx950's agent-scope fence costs several
@@ -53,7 +52,6 @@ struct DaSmem {
   static constexpr int CPR = D / 8;
   struct Loop {
     u32x4 ks[NWV][kDaTile * CPR];      // K tile, chunk c of row r at slot c ^ (r % CPR)
-    u32x4 vs[NWV][kDaTile * CPR];      // V tile, row-major
     uint32_t ps[NWV][G][kDaTile / 2];  // softmax weights, fp16 pairs of keys
   };
   struct Merge {
@@ -80,7 +78,10 @@ __global__ void __launch_bounds__(NWV * 64) decode_attn_kernel(const f16* __rest
   __shared__ DaSmem<G, D, NWV> sh;
   __shared__ float wm[NWV][G], wl[NWV][G];
   __shared__ int is_last;
-  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  // blocks in split-major order: the splits a sequence uses (split < S_eff) come first in dispatch
+  // order, so they spread over the CUs instead of sharing them with blocks that exit at once
+  const int nhb = gridDim.x / S;  // (sequence, kv head) pairs
+  const int split = blockIdx.x / nhb, hk = blockIdx.x % Hkv, b = (blockIdx.x % nhb) / Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int Hq = Hkv * G;
   const int len = min(pos[b] + 1, max_seq);
@@ -96,17 +97,15 @@ __global__ void __launch_bounds__(NWV * 64) decode_attn_kernel(const f16* __rest
   const __amdgpu_buffer_rsrc_t v_rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(Vh), (short)0, end * D * 2, 0x00020000);
 
-  // a tile's K and V rows, 1 KB per instruction straight into LDS (K swizzled so that the
-  // one-key-per-lane reads below are conflict-free, V row-major); rows at or past the split's end
-  // read as zeros through the buffer bounds.
+  // a tile's K rows, 1 KB per instruction straight into LDS, swizzled so that the one-key-per-lane
+  // reads below are conflict-free; rows at or past the split's end read as zeros through the
+  // buffer bounds.
   auto issue_tile = [&](int t0) {
 #pragma unroll
     for (int i = 0; i < kDaTile / RPI; i++) {
       const int r = i * RPI + lane / CPR, c = (lane % CPR) ^ (r % CPR);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rs, (__attribute__((address_space(3))) void*)&sh.loop.ks[wave][i * 64],
                                                16, ((t0 + r) * D + 8 * c) * 2, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rs, (__attribute__((address_space(3))) void*)&sh.loop.vs[wave][i * 64],
-                                               16, ((t0 + r) * D + 8 * (lane % CPR)) * 2, 0, 0, 0);
     }
   };
   const int t_first = start + wave * kDaTile;
@@ -130,7 +129,16 @@ __global__ void __launch_bounds__(NWV * 64) decode_attn_kernel(const f16* __rest
     const int n = min(kDaTile, end - t0);
     const bool valid = lane < n;
     if (t0 != t_first) issue_tile(t0);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile's K and V are in LDS
+    // the tile's V rows into registers (lane l: dims l*DPL..), in flight with its K rows
+    typedef typename std::conditional<DPL == 2, uint32_t, uint16_t>::type VT;
+    VT vv[kDaTile];
+#pragma unroll
+    for (int jj = 0; jj < kDaTile; jj++) {
+      const int off = ((t0 + jj) * D + lane * DPL) * 2;
+      if constexpr (DPL == 2) vv[jj] = __builtin_amdgcn_raw_buffer_load_b32(v_rs, off, 0, 0);
+      else vv[jj] = __builtin_amdgcn_raw_buffer_load_b16(v_rs, off, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K in LDS, V in registers
     __builtin_amdgcn_wave_barrier();
     u32x4 kv[CPR];
 #pragma unroll
@@ -188,8 +196,7 @@ __global__ void __launch_bounds__(NWV * 64) decode_attn_kernel(const f16* __rest
           const int j = j8 + 2 * k;
           if constexpr (DPL == 2) {
             // (v_j[d0], v_j[d1]), (v_j+1[d0], v_j+1[d1]) -> (v_j[d0], v_j+1[d0]), (v_j[d1], v_j+1[d1])
-            const uint32_t* vw = reinterpret_cast<const uint32_t*>(sh.loop.vs[wave]);
-            const uint32_t a0 = vw[j * 64 + lane], a1 = vw[(j + 1) * 64 + lane];
+            const uint32_t a0 = vv[j], a1 = vv[j + 1];
             const f16x2 v0 = as_h2(__builtin_amdgcn_perm(a1, a0, 0x05040100u));
             const f16x2 v1 = as_h2(__builtin_amdgcn_perm(a1, a0, 0x07060302u));
 #pragma unroll
@@ -198,8 +205,7 @@ __global__ void __launch_bounds__(NWV * 64) decode_attn_kernel(const f16* __rest
               o[g][1] = dot2(as_h2(pw[g][k]), v1, o[g][1]);
             }
           } else {
-            const uint16_t* vh = reinterpret_cast<const uint16_t*>(sh.loop.vs[wave]);
-            const f16x2 v0 = as_h2((uint32_t)vh[j * 64 + lane] | ((uint32_t)vh[(j + 1) * 64 + lane] << 16));
+            const f16x2 v0 = as_h2((uint32_t)vv[j] | ((uint32_t)vv[j + 1] << 16));
 #pragma unroll
             for (int g = 0; g < G; g++) o[g][0] = dot2(as_h2(pw[g][k]), v0, o[g][0]);
           }
@@ -424,7 +430,7 @@ static int decode_attn_run(const void* q, int ldq, const void* kc, const void* v
   // one sequence (kv_slot >= 0): a batch of one's split count, so every row matches that decode
   const int S = decode_splits(kv_slot >= 0 ? 1 : B, Hkv, d->cus);
   const float sl2 = 1.4426950408889634f / sqrtf((float)D);
-  const dim3 grid(S, Hkv, B);
+  const dim3 grid(S * Hkv * B);  // split-major: (split, sequence, kv head)
   int* counters = (int*)work;
   float* part = (float*)work;
   const hipStream_t st = (hipStream_t)s;
