@@ -131,8 +131,8 @@ __device__ __forceinline__ void sched_step() {
   if constexpr (ND > P) __builtin_amdgcn_sched_group_barrier(0x100, ND - P, 0);
 }
 
-template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, bool GRP = false, int BK = 64>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
+template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, bool GRP = false, int BK = 64, int KG = 1>
+__global__ void __launch_bounds__(64 * WM * WN * KG) gemm_kernel(GemmArgs g) {
   constexpr int TM = BM / WM, TN = BN / WN;          // wave tile
   constexpr int FM = TM / 32, FN = TN / 32;          // MFMA tiles per wave
   constexpr int A_ST = BM * BK;                      // halves per stage
@@ -151,14 +151,19 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   static_assert(!(GRP && Q8), "grouped (expert) GEMMs take fp16 weights");
   static_assert(BK == 128 || BK == 64 || BK == 32, "K tile depth");
   static_assert(BK != 128 || (!Q8 && !GRP), "128-deep K tiles take fp16 weights (and K % 128 == 0)");
+  static_assert(KG == 1 || (KG == 2 && !GRP), "one or two K groups (not in grouped mode)");
   // The dynamic LDS follows the static (the split-K flag below); a 16-byte element type makes the
   // compiler start it on a 16-byte boundary, which every 128-bit LDS access and DMA here needs.
   extern __shared__ u32x4 smem_raw[];
-  f16* smem = reinterpret_cast<f16*>(smem_raw);
+  // KG K groups of WM x WN waves each run the whole pipeline below on their share of the K tiles,
+  // each with its own S-stage ring; group 0 adds the other groups' sums at the end
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int kg = KG > 1 ? (tid >> 6) / NW : 0;  // this wave's K group
+  const int wave = (tid >> 6) - kg * NW;        // its index within the group
+  f16* smem = reinterpret_cast<f16*>(smem_raw) + kg * S * (A_ST + B_ST);
   f16* As = smem;               // [S][BM][64]
   f16* Bs = smem + S * A_ST;    // [S][BN][64] fp16, or [S][BN][64 bytes] int8
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int N = g.N, K = g.K;
   int M = g.M;
@@ -203,8 +208,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
   const int bm = tm * BM, bn = tn * BN;
 
   const int nkt = (K + BK - 1) / BK;
-  const int kt0 = blockIdx.y * g.kt_per_split;
-  const int nloc = min(nkt, kt0 + g.kt_per_split) - kt0;  // K tiles of this split (>= 1)
+  // K tiles of this split (>= 1), cut into KG equal runs, one per K group (the host offers KG > 1
+  // only when K % BK == 0 and the runs come out equal, so every group loops alike)
+  const int nloc = (min(nkt, (int)blockIdx.y * g.kt_per_split + g.kt_per_split) - (int)blockIdx.y * g.kt_per_split) / KG;
+  const int kt0 = blockIdx.y * g.kt_per_split + kg * nloc;
   // the last tile holds only 32 k (K % 64 == 32 with 64-deep tiles; K % 32 == 0 always)
   const bool half_tail = BK == 64 && (K & 63) != 0 && kt0 + nloc == nkt;
 
@@ -475,6 +482,29 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_kernel(GemmArgs g) {
     mfmas(1, af1, bf1, bq0);
   }
   wait_vmcnt<0>();  // the refills issued past the last tile have landed before the block ends
+  if constexpr (KG > 1) {
+    // the other group's sums to group 0 through the idle rings (element e of a wave's fragment
+    // set as one 256-byte row over its lanes), added in group order: deterministic
+    constexpr int NE = FM * FN * 16;
+    float* xf = reinterpret_cast<float*>(smem_raw);
+    barrier_no_fence();  // every wave's last fragment reads are done with the rings
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) xf[((wave * NE) + (i * FN + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[i][j][e] += xf[((wave * NE) + (i * FN + j) * 16 + e) * 64 + lane];
+  }
 
   // ---- result layout (W fragment as the MFMA's first operand): lane (fk, fr) of tile (i, j) holds
   //      row fr of the tile's 32 rows, columns 8 g + 4 fk + 0..3 in acc[i][j][4 g .. 4 g + 3]:
@@ -579,7 +609,8 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(const float* __restric
   store4(dst, o, vec_c);
 }
 
-// Tile configurations: {BM, BN, WM, WN, stages, BK}; WM x WN waves per block, BK-deep K tiles. The
+// Tile configurations: {BM, BN, WM, WN, stages, BK[, K groups]}; WM x WN waves per K group, BK-deep
+// K tiles. The
 // 32-deep ones give the big 8-wave tiles four (or six) stages in the same LDS as two 64-deep
 // ones: more K tiles in flight to cover the global->LDS latency. 128 x 160 and 128 x 96 (four
 // waves stacked along M, each 32 rows by the whole width) cut N = 5120 and N = 3072 at M = 1024
@@ -588,9 +619,14 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(const float* __restric
 // 256 x 192 (eight waves of 64 x 96) cuts N = 3072 at M = 1024 into 64 big tiles, 256 blocks with
 // a 4-way split-K: half the staged bytes of 128 x 96 for the same K range. The two 128-deep small
 // tiles (fp16 weights, K % 128 == 0) fetch each W row in 256-byte runs per K tile instead of
-// 128-byte ones, for the weight-streaming small-M shapes.
+// 128-byte ones, for the weight-streaming small-M shapes. The last, 128 x 160 in two K groups
+// (eight waves: two 4-wave pipelines on the two halves of the K tiles, each with its own 2-stage
+// ring, group 1's sums handed to group 0 through LDS at the end), puts two waves on each SIMD
+// for the same one-tile-per-CU cut of N = 5120: QKV of Llama-3.2-3B at M = 1024 in 42.3 against
+// 45.6 us. The same split of 128 x 96 (o, down) measured no faster: those tiles are bound by the
+// LDS reads of the W rows every wave re-reads, not by latency.
 struct GemmCfg {
-  int bm, bn, wm, wn, st, bk;
+  int bm, bn, wm, wn, st, bk, kg = 1;  // kg: K groups of wm x wn waves (two waves on each SIMD at kg 2)
 };
 constexpr GemmCfg kGemmCfgs[] = {{256, 256, 2, 2, 2, 64}, {256, 128, 2, 2, 3, 64}, {128, 256, 2, 2, 3, 64},
                                  {64, 128, 2, 2, 4, 64},  {128, 128, 2, 2, 2, 64}, {64, 64, 2, 2, 4, 64},
@@ -598,7 +634,7 @@ constexpr GemmCfg kGemmCfgs[] = {{256, 256, 2, 2, 2, 64}, {256, 128, 2, 2, 3, 64
                                  {256, 128, 2, 4, 3, 64}, {256, 256, 2, 4, 4, 32}, {256, 128, 2, 2, 6, 32},
                                  {128, 256, 2, 4, 6, 32}, {128, 160, 4, 1, 4, 64}, {128, 96, 4, 1, 4, 64},
                                  {32, 256, 1, 4, 4, 64},  {256, 192, 4, 2, 2, 64}, {64, 128, 2, 2, 3, 128},
-                                 {128, 64, 2, 2, 3, 128}};
+                                 {128, 64, 2, 2, 3, 128}, {128, 160, 4, 1, 2, 64, 2}};
 constexpr int kGemmNumCfgs = sizeof(kGemmCfgs) / sizeof(kGemmCfgs[0]);
 // A config exists for a weight format when its A and W tiles split into whole 1 KB DMA
 // instructions per wave (int8 W rows are half as wide: 128 x 160 and 128 x 96 are fp16 only).
@@ -609,24 +645,25 @@ constexpr bool gemm_cfg_ok(int c, bool q8) {
 }
 // ... and for a shape: 128-deep tiles have no K tail, so they need K % 128 == 0.
 constexpr bool gemm_cfg_fits(int c, bool q8, int K) {
-  return gemm_cfg_ok(c, q8) && (kGemmCfgs[c].bk < 128 || K % 128 == 0);
+  return gemm_cfg_ok(c, q8) && (kGemmCfgs[c].bk < 128 || K % 128 == 0) &&
+         (kGemmCfgs[c].kg == 1 || (K % kGemmCfgs[c].bk == 0 && (K / kGemmCfgs[c].bk) % kGemmCfgs[c].kg == 0));
 }
 constexpr int kGemmGrpCfg = 3;  // the grouped (MoE expert) GEMM's tile: 64 x 128
 inline size_t gemm_lds_bytes(int cfg, bool q8) {
   const GemmCfg& c = kGemmCfgs[cfg];
-  return (size_t)c.st * (c.bm * c.bk * 2 + c.bn * (q8 ? c.bk : 2 * c.bk));
+  return (size_t)c.kg * c.st * (c.bm * c.bk * 2 + c.bn * (q8 ? c.bk : 2 * c.bk));
 }
 
-template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, int BK>
+template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, int BK, int KG>
 int gemm_launch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
   const size_t lds = gemm_lds_bytes(cfg, Q8);
-  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WM, WN, S, EPI, Q8, false, BK>);
-  const int bpc = hi_blocks_per_cu(fn, 64 * WM * WN, lds);  // also lifts the dynamic-LDS limit
+  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WM, WN, S, EPI, Q8, false, BK, KG>);
+  const int bpc = hi_blocks_per_cu(fn, 64 * WM * WN * KG, lds);  // also lifts the dynamic-LDS limit
   if (bpc < 0) return -2;
   if (bpc == 0) HI_FAIL("gemm: tile %dx%d does not fit on a CU", BM, BN);
   const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, EPI, Q8, false, BK>), dim3(tiles, splits), dim3(64 * WM * WN), lds,
-                     s, g);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, EPI, Q8, false, BK, KG>), dim3(tiles, splits),
+                     dim3(64 * WM * WN * KG), lds, s, g);
   HI_TRY(hipGetLastError());
   if (splits > 1) {
     const int64_t quads = (int64_t)g.M * (EPI == 2 ? g.N / 2 : g.N) / 4;
@@ -646,22 +683,22 @@ int gemm_blocks_per_cu(int cfg, bool q8);
 
 #define HI_GEMM_K(i, q)                                                                                        \
   gemm_kernel<kGemmCfgs[i].bm, kGemmCfgs[i].bn, kGemmCfgs[i].wm, kGemmCfgs[i].wn, kGemmCfgs[i].st, EPI, q, false, \
-              kGemmCfgs[i].bk>
+              kGemmCfgs[i].bk, kGemmCfgs[i].kg>
 #define HI_GEMM_CFG(i, q)                                                                                      \
   if constexpr (gemm_cfg_ok(i, q)) {                                                                           \
     if (cfg == i && q8 == q)                                                                                   \
       return gemm_launch<kGemmCfgs[i].bm, kGemmCfgs[i].bn, kGemmCfgs[i].wm, kGemmCfgs[i].wn, kGemmCfgs[i].st, EPI, \
-                         q, kGemmCfgs[i].bk>(g, cfg, splits, s);                                               \
+                         q, kGemmCfgs[i].bk, kGemmCfgs[i].kg>(g, cfg, splits, s);                              \
   }
 #define HI_GEMM_OCC(i)                                                                                         \
   if constexpr (gemm_cfg_ok(i, true))                                                                          \
     if (cfg == i && q8)                                                                                        \
       return hi_blocks_per_cu(reinterpret_cast<const void*>(&HI_GEMM_K(i, true)),                              \
-                              64 * kGemmCfgs[i].wm * kGemmCfgs[i].wn, gemm_lds_bytes(i, true));                \
+                              64 * kGemmCfgs[i].wm * kGemmCfgs[i].wn * kGemmCfgs[i].kg, gemm_lds_bytes(i, true)); \
   if constexpr (gemm_cfg_ok(i, false))                                                                         \
     if (cfg == i && !q8)                                                                                       \
       return hi_blocks_per_cu(reinterpret_cast<const void*>(&HI_GEMM_K(i, false)),                             \
-                              64 * kGemmCfgs[i].wm * kGemmCfgs[i].wn, gemm_lds_bytes(i, false));
+                              64 * kGemmCfgs[i].wm * kGemmCfgs[i].wn * kGemmCfgs[i].kg, gemm_lds_bytes(i, false));
 #define HI_GEMM_DEFINE_RUN(EPIV)                                                                               \
   template <>                                                                                                  \
   int gemm_run<EPIV>(const GemmArgs& g, int cfg, int splits, bool q8, hipStream_t s) {                        \
@@ -670,11 +707,12 @@ int gemm_blocks_per_cu(int cfg, bool q8);
     HI_GEMM_CFG(4, false) HI_GEMM_CFG(5, false) HI_GEMM_CFG(6, false) HI_GEMM_CFG(7, false)                    \
     HI_GEMM_CFG(8, false) HI_GEMM_CFG(9, false) HI_GEMM_CFG(10, false) HI_GEMM_CFG(11, false)                  \
     HI_GEMM_CFG(12, false) HI_GEMM_CFG(13, false) HI_GEMM_CFG(14, false) HI_GEMM_CFG(15, false)                \
-    HI_GEMM_CFG(16, false) HI_GEMM_CFG(17, false) HI_GEMM_CFG(18, false)                                       \
+    HI_GEMM_CFG(16, false) HI_GEMM_CFG(17, false) HI_GEMM_CFG(18, false) HI_GEMM_CFG(19, false)                \
     HI_GEMM_CFG(0, true) HI_GEMM_CFG(1, true) HI_GEMM_CFG(2, true) HI_GEMM_CFG(3, true)                        \
     HI_GEMM_CFG(4, true) HI_GEMM_CFG(5, true) HI_GEMM_CFG(6, true) HI_GEMM_CFG(7, true)                        \
     HI_GEMM_CFG(8, true) HI_GEMM_CFG(9, true) HI_GEMM_CFG(10, true) HI_GEMM_CFG(11, true) HI_GEMM_CFG(12, true) \
     HI_GEMM_CFG(13, true) HI_GEMM_CFG(14, true) HI_GEMM_CFG(15, true) HI_GEMM_CFG(16, true)                   \
+    HI_GEMM_CFG(19, true)                                                                                      \
     HI_FAIL("gemm: no kernel for config %d", cfg);                                                             \
   }                                                                                                            \
   template <>                                                                                                  \
@@ -683,5 +721,6 @@ int gemm_blocks_per_cu(int cfg, bool q8);
     HI_GEMM_OCC(0) HI_GEMM_OCC(1) HI_GEMM_OCC(2) HI_GEMM_OCC(3) HI_GEMM_OCC(4) HI_GEMM_OCC(5) HI_GEMM_OCC(6)    \
     HI_GEMM_OCC(7) HI_GEMM_OCC(8) HI_GEMM_OCC(9) HI_GEMM_OCC(10) HI_GEMM_OCC(11) HI_GEMM_OCC(12)              \
     HI_GEMM_OCC(13) HI_GEMM_OCC(14) HI_GEMM_OCC(15) HI_GEMM_OCC(16) HI_GEMM_OCC(17) HI_GEMM_OCC(18)            \
+    HI_GEMM_OCC(19)                                                                                            \
     return -1;                                                                                                 \
   }

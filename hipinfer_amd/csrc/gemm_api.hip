@@ -50,7 +50,7 @@ int cfg_blocks_per_cu(int cfg, bool q8) {
 
 // Relative MFMA efficiency of each tile shape (bigger tiles reuse more of what they stage).
 constexpr double kCfgEff[kGemmNumCfgs] = {0.9, 0.85, 0.85, 0.6, 0.8, 0.45, 0.4, 0.6,
-                                           1.0, 0.9, 1.05, 0.85, 0.95, 0.85, 0.8, 0.5, 0.95, 0.6, 0.6};
+                                           1.0, 0.9, 1.05, 0.85, 0.95, 0.85, 0.8, 0.5, 0.95, 0.6, 0.6, 0.95};
 
 struct Choice {
   int cfg, splits;
@@ -72,7 +72,7 @@ Choice gemm_pick(int M, int N, int K, bool q8, int cus) {
     const double tiles = (double)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int slots = cus * cfg_blocks_per_cu(c, q8);
     for (int sp = 1; sp <= 8; sp += sp < 6 ? 1 : 2) {
-      if (sp > nkt || (sp > 1 && tiles * sp > 4.0 * cus) || tiles > kMaxTiles) continue;
+      if (sp > nkt || (sp > 1 && (tiles * sp > 4.0 * cus || kGemmCfgs[c].kg > 1)) || tiles > kMaxTiles) continue;
       const int kps = (nkt + sp - 1) / sp;
       const double rounds = std::ceil(tiles * sp / slots);
       const double t_mfma = rounds * 2.0 * bm * bn * kps * bk / (mfma_per_cu * kCfgEff[c]);
@@ -192,7 +192,7 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
     const long tiles = (long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn);
     if (bm > 2 * mb && kGemmCfgs[c].bm != 32) continue;  // a tile far taller than M only stages padding
     for (int sp = 1; sp <= 8 && !rc; sp += sp < 6 ? 1 : 2) {
-      if (sp > nkt || (sp > 1 && tiles * sp > 4L * d->cus) || tiles > kMaxTiles) continue;
+      if (sp > nkt || (sp > 1 && (tiles * sp > 4L * d->cus || kGemmCfgs[c].kg > 1)) || tiles > kMaxTiles) continue;
       float us = 0.f;
       rc = time_it({c, sp}, std::max(nrot, 4), &us);
       if (!rc) timed.push_back({us, {c, sp}});
@@ -239,6 +239,7 @@ int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s
   GemmArgs g = g0;
   const int nkt = (g.K + kGemmCfgs[ch.cfg].bk - 1) / kGemmCfgs[ch.cfg].bk;  // K tiles of the chosen depth
   if (ch.splits > nkt) ch.splits = nkt;
+  if (kGemmCfgs[ch.cfg].kg > 1) ch.splits = 1;  // a K-group tile splits K inside the block
   int kps = (nkt + ch.splits - 1) / ch.splits;
   ch.splits = (nkt + kps - 1) / kps;  // no empty splits
   const int bm = kGemmCfgs[ch.cfg].bm, bn = kGemmCfgs[ch.cfg].bn;
@@ -428,7 +429,7 @@ HI_EXPORT int hi_gemm_last_choice(int* cfg, int* splits) {
 }
 HI_EXPORT int hi_gemm_config_desc(int c, char* out, int n) {
   if (c < 0 || c >= kGemmNumCfgs || !out || n < 1) return -1;
-  snprintf(out, n, "mfma 32x32x16 %dx%dx%d waves %dx%d stages %d", kGemmCfgs[c].bm, kGemmCfgs[c].bn, kGemmCfgs[c].bk,
-           kGemmCfgs[c].wm, kGemmCfgs[c].wn, kGemmCfgs[c].st);
+  snprintf(out, n, "mfma 32x32x16 %dx%dx%d waves %dx%dx%d stages %d", kGemmCfgs[c].bm, kGemmCfgs[c].bn, kGemmCfgs[c].bk,
+           kGemmCfgs[c].wm, kGemmCfgs[c].wn, kGemmCfgs[c].kg, kGemmCfgs[c].st);
   return 0;
 }

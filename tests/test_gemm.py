@@ -60,7 +60,7 @@ def gemm_check(hi, O, name, A, W, r, epi=0, bias=None, scales=None, res=None, to
 
 # The library's tile-config count. Not read from the library at collection time: libhipinfer.so must
 # be loaded after torch has initialised its HIP runtime. test_config_count_is_current keeps it honest.
-NUM_CFGS = 19
+NUM_CFGS = 20
 # every tile configuration, and the automatic choice (-1)
 CFGS = list(range(-1, NUM_CFGS))
 
@@ -82,13 +82,13 @@ def last_choice(hi):
 
 
 def cfg_shape(hi, cfg):
-    """(bm, bn, bk, waves) of a tile config, from hi_gemm_config_desc."""
+    """(bm, bn, bk, waves per K group, K groups) of a tile config, from hi_gemm_config_desc."""
     import ctypes
     import re
     buf = ctypes.create_string_buffer(128)
     hi.lib.hi_gemm_config_desc(cfg, buf, 128)
-    m = re.search(r"(\d+)x(\d+)x(\d+) waves (\d+)x(\d+)", buf.value.decode())
-    return int(m[1]), int(m[2]), int(m[3]), int(m[4]) * int(m[5])
+    m = re.search(r"(\d+)x(\d+)x(\d+) waves (\d+)x(\d+)x(\d+)", buf.value.decode())
+    return int(m[1]), int(m[2]), int(m[3]), int(m[4]) * int(m[5]), int(m[6])
 
 
 def cfg_runs(hi, cfg, q8, K):
@@ -96,10 +96,11 @@ def cfg_runs(hi, cfg, q8, K):
     every wave issues whole 1 KB DMA instructions per K tile for the A tile and the W tile (int8 W rows
     are half as wide), and the 128-deep tiles take fp16 weights with K % 128 == 0; otherwise the
     automatic choice runs instead."""
-    bm, bn, bk, nw = cfg_shape(hi, cfg)
+    bm, bn, bk, nw, kg = cfg_shape(hi, cfg)
     a, b = bm * 2 * bk, bn * (bk if q8 else 2 * bk)
     ok = a % (1024 * nw) == 0 and b % (1024 * nw) == 0 and a >= 1024 * nw and b >= 1024 * nw
-    return ok and (bk < 128 or (not q8 and K % 128 == 0))
+    # K groups split the K tiles evenly inside the block: K a whole number of tiles, per group too
+    return ok and (bk < 128 or (not q8 and K % 128 == 0)) and (kg == 1 or (K % bk == 0 and (K // bk) % kg == 0))
 
 
 def assert_ran(hi, cfg, q8, K, what):
