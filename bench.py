@@ -761,7 +761,57 @@ def gemm_counters(csv_path, cus=256, xcds=8, replays=3):
               f"{wait:.1f} | {active / a['n']:.0f} |")
 
 
+def gemv_counters(csv_paths, layers=28):
+    """Per-kind counters of `bench.py --profile c4` (the C4 GEMV set at 8 rows, fp16 tokens then int8
+    tokens), from one or more rocprofv3 `--pmc` counter CSVs of the same command (one counter pass
+    each). A token is `layers` x (QKV, o, gate/up, down) + lm_head GEMV launches in that order, so a
+    launch's kind is its position in its token; o and down share one kernel instance and are told
+    apart this way. Sums every token's launches per (kind, format). Prints a markdown table."""
+    import csv
+    kinds = ["qkv", "o", "gate_up", "down"]
+    per_token = layers * 4 + 1
+    agg = {}
+    for path in csv_paths:
+        disp = {}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if "gemv_kernel" not in r["Kernel_Name"]:
+                    continue
+                d = disp.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"]})
+                d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        for i, d_id in enumerate(sorted(disp)):
+            d = disp[d_id]
+            j = i % per_token
+            kind = "lm_head" if j == per_token - 1 else kinds[j % 4]
+            # the format is the kernel's WF template argument (0 fp16, 1 int8): 4th of <MR, NORM, EPI, WF, G>
+            args = d["name"][d["name"].find("<") + 1:d["name"].find(">")].split(",")
+            fmt = "int8" if args[3].strip() != "0" else "fp16"
+            a = agg.setdefault((kind, fmt), {"name": d["name"], "n": {}})
+            for c, v in d.items():
+                if c != "name":
+                    a[c] = a.get(c, 0.0) + v
+                    a["n"][c] = a["n"].get(c, 0) + 1
+    print("| kind | format | kernel | launches | VALU instructions per wave | VALU busy / wave cycles % "
+          "| LDS instructions per wave | LDS wait / wave cycles % | FETCH_SIZE KiB per launch |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for fmt in ("fp16", "int8"):
+        for kind in kinds + ["lm_head"]:
+            a = agg.get((kind, fmt))
+            if not a:
+                continue
+            w, wc = a.get("SQ_WAVES", 0), a.get("SQ_WAVE_CYCLES", 0)
+            n = max(a["n"].values())
+            name = a["name"][a["name"].find("gemv_kernel"):a["name"].find(">") + 1]
+            fetch = a.get("FETCH_SIZE", 0) / max(1, a["n"].get("FETCH_SIZE", 1))
+            print(f"| {kind} | {fmt} | `{name}` | {n} | {a.get('SQ_INSTS_VALU', 0) / max(1, w):.0f} | "
+                  f"{100 * a.get('SQ_ACTIVE_INST_VALU', 0) / max(1, wc):.1f} | {a.get('SQ_INSTS_LDS', 0) / max(1, w):.0f} | "
+                  f"{100 * a.get('SQ_WAIT_INST_LDS', 0) / max(1, wc):.1f} | {fetch:.0f} |")
+
+
 def main():
+    if len(sys.argv) >= 3 and sys.argv[1] == "--gemv-counters":
+        gemv_counters(sys.argv[2:])
+        return
     if len(sys.argv) == 3 and sys.argv[1] == "--timeline":
         timeline(sys.argv[2])
         return
