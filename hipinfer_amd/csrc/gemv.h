@@ -81,7 +81,10 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   // overlap more of the item's latency (int8 o / down: 5.24 / 11.32 us against 5.31 / 11.39). From 4
   // activation rows on, the SwiGLU launches take the smaller step too: it frees the registers for a
   // second block per CU (C4 gate/up at 8 rows: fp16 13.6 against 14.7 us, int8 14.4 against 14.7).
-  constexpr int UN = (EPI == 2 ? (MR >= 4 ? 4 : 8) : (EPI == 1 && WF == WF_I8) ? 2 : 4) * (WF == WF_I8H ? 2 : 1);
+  // The one-row plain launch (lm_head: waves stream about 16 items each) takes the larger step:
+  // fp16 152.7 against 156.2 us (a step twice as large again: 153.0; int8 79.9 against 80.2).
+  constexpr int UN = (EPI == 2 ? (MR >= 4 ? 4 : 8) : (EPI == 0 && MR == 1) ? 8 : (EPI == 1 && WF == WF_I8) ? 2 : 4) *
+                     (WF == WF_I8H ? 2 : 1);
   constexpr int U = UN / R > 0 ? UN / R : 1;
   constexpr int SW = 64 * U;                            // chunks of a row per step
   constexpr int XC = MR <= 8 ? (MR <= 4 ? 4 / MR : 1) : 0;  // activation chunks per row held in registers
