@@ -30,9 +30,10 @@ static int gemv_common(GemvArgs a, int epi, hipStream_t s, const char* who) {
   if (a.scales && !aligned(a.scales, 2)) HI_FAIL("%s: scales must be 2-byte aligned", who);
   const int n_out = epi == 2 ? a.N / 2 : a.N;
   if (epi != 3 && a.ldo < n_out) HI_FAIL("%s: ldo %lld < %d output columns", who, (long long)a.ldo, n_out);
-  // LDS per activation row: the row, its per-wave norm partials, and for int8 weights one partial
-  // sum per staging thread
-  const size_t row_lds = (size_t)a.K * 2 + kGemvWaves * sizeof(float) + (wf != WF_F16 ? kGemvThreads * sizeof(float) : 0);
+  // LDS per activation row: the row, its per-wave norm partials and inverse RMS, and for int8
+  // weights one partial sum per staging thread
+  const size_t row_lds =
+      (size_t)a.K * 2 + (kGemvWaves + 1) * sizeof(float) + (wf != WF_F16 ? kGemvThreads * sizeof(float) : 0);
   if (row_lds > (size_t)d->lds_max) HI_FAIL("%s: K=%d activation row exceeds LDS", who, a.K);
 
   const bool norm = a.normw != nullptr;

@@ -93,6 +93,14 @@ HI_EXPORT int hi_device_cus() {
   return d ? d->cus : -2;
 }
 
+// The largest dynamic LDS one block may opt into on the current device (the reference's
+// hi_max_smem, api.cu:49: its shared-memory opt-in, which sizes the fused-norm GEMV's rows; on
+// MI355X the CU's 160 KB LDS); -2 on a HIP error.
+HI_EXPORT int hi_max_smem() {
+  const HiDevice* d = hi_device();
+  return d ? d->lds_max : -2;
+}
+
 // ------------------------------------------------------------------ quantiser
 // One wave per row. VEC: 16-byte loads (K % 8 == 0, 16-byte aligned rows), else 2-byte loads.
 template <bool VEC>

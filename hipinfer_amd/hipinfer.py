@@ -50,6 +50,7 @@ int hi_gemv_qkv_rope_w8(ptr x, int ldx, ptr normw, float eps, ptr W, ptr scales,
 int hi_quantize_rows(ptr w, i64 N, int K, ptr q, ptr s, ptr stream);
 int hi_dequantize_rows(ptr q, ptr s, i64 N, int K, ptr out, ptr stream);
 int hi_device_cus();
+int hi_max_smem();
 int hi_gemm(ptr A, int lda, ptr W, ptr bias, ptr C, int ldc, int M, int N, int K, int epi, ptr stream);
 int hi_gemm_w8(ptr A, int lda, ptr W, ptr scales, ptr bias, ptr C, int ldc, int M, int N, int K, int epi, ptr stream);
 int hi_gemm_force_config(int cfg);

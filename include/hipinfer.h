@@ -161,6 +161,9 @@ int hi_dequantize_rows(const void* q, const void* s, long long N, int K, void* o
 
 /* Compute units of the current device (diagnostics; the launchers size their grids from it). */
 int hi_device_cus(void);
+/* Largest dynamic LDS (bytes) a block may opt into on the current device: 160 KB on MI355X.
+ * Replaces api.cu:49 (hi_max_smem, the CUDA shared-memory opt-in). */
+int hi_max_smem(void);
 
 /* ---- engine: weight-file loader, prefill, graph-captured greedy decode (one GPU)
  * An opaque engine over a weight file in the reference's export format (scripts/export.py:5-38;

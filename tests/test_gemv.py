@@ -233,6 +233,23 @@ def test_strides_chunking_and_odd_sizes(hi, O):
     check("K=8 N=1", host(hi.gemv(cuda(x), cuda(W))), O.gemv(x, W), 2e-3, 2e-3)
 
 
+def test_max_smem_bounds_the_activation_rows(hi, O):
+    """hi_max_smem (the reference's api.cu:49) reports the LDS a block may opt into. The GEMV stages
+    its activation rows there: rows that do not fit together run in chunks (each row unchanged, checked
+    against the oracle), and a single row longer than the LDS is refused cleanly."""
+    import torch
+    lim = hi.lib.hi_max_smem()
+    assert lim >= 64 * 1024 and lim % 1024 == 0, lim
+    r = rng(31)
+    K = (lim // 2 // 8 - 640) * 8  # one row fits, sixteen do not
+    assert 16 * K * 2 > lim
+    x, W = h16(r, 16, K), (r.standard_normal((32, K)) * 0.02).astype(np.float16)
+    check("16 rows in chunks", host(hi.gemv(cuda(x), cuda(W))), O.gemv(x, W), 3e-3, 3e-3)
+    K = (lim // 2 // 8 + 8) * 8  # one row alone is longer than the LDS
+    with pytest.raises(Exception):
+        hi.gemv(torch.zeros(1, K, dtype=torch.float16, device="cuda"), torch.zeros(16, K, dtype=torch.float16, device="cuda"))
+
+
 def test_rejects_bad_arguments(hi):
     import torch
     x = torch.zeros(1, 12, dtype=torch.float16, device="cuda")
