@@ -719,46 +719,85 @@ def timeline(csv_path):
     print(f"| all | {per_token} | | | {tb:.1f} | {tg:.1f} |")
 
 
-def gemm_counters(csv_path, cus=256, xcds=8, replays=3):
-    """Per-GEMM-kind counters of the last `replays` layer passes of `bench.py --profile gemm`, from a
-    rocprofv3 `--pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_BUSY_CYCLES
-    SQ_WAVE_CYCLES SQ_WAIT_INST_ANY` counter CSV: MfmaUtil = 100 * SQ_VALU_MFMA_BUSY_CYCLES /
-    (GRBM_GUI_ACTIVE * CUs * 4), rocprofv3's own derived metric, with GRBM_GUI_ACTIVE taken per XCD
-    (the raw counter is the sum of the 8 XCDs' copies). A pass is 28 layers x (QKV, o, gate/up,
-    down) GEMM launches, in that order. Prints a markdown table."""
+def gemm_counters(csv_paths, cus=256, xcds=8, replays=3):
+    """Per-GEMM-kind counters of the last `replays` layer passes of `bench.py --profile gemm`, from one
+    or more rocprofv3 `--pmc` counter CSVs of that command (one counter pass each; every pass also
+    collects GRBM_GUI_ACTIVE). A pass is 28 layers x (QKV, o, gate/up, down) GEMM launches, in that
+    order, so a launch's kind is its position. Prints up to two markdown tables:
+      * MfmaUtil = 100 * SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * CUs * 4), rocprofv3's own
+        derived metric, with GRBM_GUI_ACTIVE taken per XCD (the raw counter is the sum of the 8 XCDs'
+        copies), the MFMA flop count (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512) and SQ_WAIT_INST_ANY;
+      * the memory path (when its counters were collected): LDS indexed-access cycles, bank and
+        address conflict cycles, TA busy, TD busy and TD stalled on the TC, TCP tag lookups, tag
+        conflicts and waits for L2 data, each per CU per GPU-active cycle."""
     import csv
-    disp = {}
-    with open(csv_path) as f:
-        for r in csv.DictReader(f):
-            if "gemm_kernel" not in r["Kernel_Name"]:
-                continue
-            d = disp.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"]})
-            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
-    ids = sorted(disp)
-    per_pass = P_L * 4
-    last = ids[-replays * per_pass:]
     kinds = ["qkv", "o", "gate_up", "down"]
-    agg = {k: {"n": 0} for k in kinds}
-    for i, d_id in enumerate(last):
-        a = agg[kinds[i % 4]]
-        a["n"] += 1
-        a["name"] = disp[d_id]["name"]
-        for c, v in disp[d_id].items():
-            if c != "name":
+    agg = {k: {"n": {}} for k in kinds}
+    total = 0
+    passes = {}  # path -> the counters it collected
+    for path in ([csv_paths] if isinstance(csv_paths, str) else csv_paths):
+        disp = {}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if "gemm_kernel" not in r["Kernel_Name"]:
+                    continue
+                d = disp.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"]})
+                d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+                passes.setdefault(path, set()).add(r["Counter_Name"])
+        ids = sorted(disp)
+        total = len(ids)
+        last = ids[-replays * P_L * 4:]
+        for i, d_id in enumerate(last):
+            a = agg[kinds[i % 4]]
+            a["name"] = disp[d_id]["name"]
+            for c, v in disp[d_id].items():
+                if c == "name":
+                    continue
+                if c == "GRBM_GUI_ACTIVE":  # the same per pass: keep one pass's
+                    c = "GRBM_GUI_ACTIVE@" + path
                 a[c] = a.get(c, 0.0) + v
-    print(f"dispatches: {len(ids)} gemm_kernel launches in the trace; the last {len(last)} ({replays} passes) used")
-    print("| GEMM | kernel | MfmaUtil % | MFMA flop per launch (MOPs x 512) | SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES % "
-          "| GPU-active cycles per launch (per XCD) |")
-    print("|---|---|---|---|---|---|")
-    for k in kinds:
-        a = agg[k]
-        active = a.get("GRBM_GUI_ACTIVE", 0) / xcds
-        util = 100 * a.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) / max(1.0, active * cus * 4)
-        wait = 100 * a.get("SQ_WAIT_INST_ANY", 0) / max(1.0, a.get("SQ_WAVE_CYCLES", 0))
-        name = a.get("name", "")
-        name = name[name.find("gemm_kernel"):][:60]
-        print(f"| {k} | `{name}` | {util:.1f} | {a.get('SQ_INSTS_VALU_MFMA_MOPS_F16', 0) * 512 / a['n']:.4g} | "
-              f"{wait:.1f} | {active / a['n']:.0f} |")
+                a["n"][c] = a["n"].get(c, 0) + 1
+
+    def active(a, counter):
+        # GPU-active cycles (per XCD) summed over the kind's launches, from the pass that has `counter`
+        for c in a:
+            if c.startswith("GRBM_GUI_ACTIVE@") and counter in passes.get(c.split("@", 1)[1], ()):
+                return a[c] / xcds
+        return max(1.0, next((a[c] for c in a if c.startswith("GRBM_GUI_ACTIVE@")), 1.0) / xcds)
+
+    print(f"dispatches: {total} gemm_kernel launches in the trace; the last {replays * P_L * 4} ({replays} passes) used")
+    if any("SQ_VALU_MFMA_BUSY_CYCLES" in agg[k] for k in kinds):
+        print("| GEMM | kernel | MfmaUtil % | MFMA flop per launch (MOPs x 512) | SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES % "
+              "| GPU-active cycles per launch (per XCD) |")
+        print("|---|---|---|---|---|---|")
+        for k in kinds:
+            a = agg[k]
+            act = active(a, "SQ_VALU_MFMA_BUSY_CYCLES")
+            n = max(1, a["n"].get("SQ_VALU_MFMA_BUSY_CYCLES", 1))
+            util = 100 * a.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) / max(1.0, act * cus * 4)
+            wait = 100 * a.get("SQ_WAIT_INST_ANY", 0) / max(1.0, a.get("SQ_WAVE_CYCLES", 0))
+            name = a.get("name", "")
+            name = name[name.find("gemm_kernel"):][:60]
+            mops = a.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0) * 512 / n
+            print(f"| {k} | `{name}` | {util:.1f} | {mops:.4g} | {wait:.1f} | {act / n:.0f} |")
+    mem = ["SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_ADDR_CONFLICT", "TA_BUSY_avr", "TD_TD_BUSY_sum",
+           "TD_TC_STALL_sum", "TCP_TOTAL_CACHE_ACCESSES_sum", "TCP_READ_TAGCONFLICT_STALL_CYCLES_sum",
+           "TCP_PENDING_STALL_CYCLES_sum"]
+    have = [c for c in mem if any(c in agg[k] for k in kinds)]
+    if have:
+        print()
+        print("| GEMM | " + " | ".join(have) + " |")
+        print("|---|" + "---|" * len(have))
+        for k in kinds:
+            a = agg[k]
+            row = []
+            for c in have:
+                act = active(a, c)
+                # TA_BUSY_avr is an average over the TA instances (one per CU): per GPU-active cycle;
+                # the others are sums over CUs: per CU per GPU-active cycle
+                v = a.get(c, 0.0) / max(1.0, act if c == "TA_BUSY_avr" else act * cus)
+                row.append(f"{v:.3f}")
+            print(f"| {k} | " + " | ".join(row) + " |")
 
 
 def gemv_counters(csv_paths, layers=28):
@@ -815,8 +854,8 @@ def main():
     if len(sys.argv) == 3 and sys.argv[1] == "--timeline":
         timeline(sys.argv[2])
         return
-    if len(sys.argv) == 3 and sys.argv[1] == "--gemm-counters":
-        gemm_counters(sys.argv[2])
+    if len(sys.argv) >= 3 and sys.argv[1] == "--gemm-counters":
+        gemm_counters(sys.argv[2:])
         return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
