@@ -10,8 +10,9 @@
 //    combines) and streams it with 128-bit nontemporal buffer loads (the weights are read once),
 //    lane l taking 16-byte chunks l, l+64, ...; the unit is cut into steps, and two register sets
 //    alternate so that the next step (of this unit or the wave's next one) is always in flight
-//    while the current one is computed: the first step goes out before the activation prologue,
-//    and the wave's memory pipe never idles behind its own compute, reductions or epilogues;
+//    while the current one is computed: the first step (the first two for the one-row fp16
+//    gate/up and lm_head launches) goes out before the activation prologue, and the wave's memory
+//    pipe never idles behind its own compute, reductions or epilogues;
 //  * a step's epilogue inputs (row scales, residual, bias, RoPE table entry) travel with its
 //    weights, and every memory instruction runs on every path (buffer bounds turn the tails and
 //    the step past a wave's last unit into zero reads, dropped stores replace skipped ones), so
@@ -27,6 +28,8 @@
 // bit-identical to the 1-row GEMV of that row (the reference's promise, api.cu:153-155, that
 // speculative verification relies on).
 #pragma once
+#include <type_traits>
+
 #include "hi_common.h"
 
 // Weight formats: fp16; int8 streamed 16 weights per 16-byte load (K % 16 == 0); int8 streamed
@@ -195,6 +198,20 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   Pre pa[G] = {}, pb[G] = {};
   int t = wave < a.ipb ? blockIdx.x * a.ipb + wave : n_items, s = 0;  // the step in flight in (wa, pa)
   issue(wa, pa, t, 0);
+  // The one-row fp16 SwiGLU and plain launches (gate/up, lm_head: waves stream several items)
+  // also issue the step after it here, so two steps are in flight through the prologue: measured
+  // on MI355X at Llama-3.1-8B shapes, gate/up 36.7 against 37.2 us. The launches that request
+  // their whole share in one or two steps (QKV, o, the int8 ones) ran slower that way (fp16 QKV
+  // 10.46 against 10.11 us, int8 QKV 8.57 against 7.42): a larger first burst of requests.
+  constexpr bool PRE = MR == 1 && WF == WF_F16 && (EPI == 0 || EPI == 2);
+  if constexpr (PRE) {
+    int t1 = t, s1 = 1;
+    if (s1 == SPI) {
+      s1 = 0;
+      t1 += nw;
+    }
+    issue(wb, pb, t1, s1);
+  }
   // ---- 3. stage the activation rows in LDS, RMSNorm'd (HF order) when normw is given; rows >= M
   //         are zero so no garbage reaches the sums. Thread t stages chunks t, t + 512, ... of
   //         every row, in that order on every path, and (int8) sums each row's chunks as it goes.
@@ -367,7 +384,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
   const uint32_t out_bytes = (uint32_t)(((int64_t)(M - 1) * a.ldo + n_out) * 2);
   const RS out_rs = __builtin_amdgcn_make_buffer_rsrc(a.out, (short)0, (int)out_bytes, kRawBuffer);
 
-  auto stage = [&](LT (&cur)[R][U], Pre (&pc)[G], LT (&nxt)[R][U], Pre (&pn)[G]) {
+  auto stage = [&](auto issue_next, LT (&cur)[R][U], Pre (&pc)[G], LT (&nxt)[R][U], Pre (&pn)[G]) {
     t = __builtin_amdgcn_readfirstlane(t);  // wave-uniform: keeps every buffer resource in SGPRs
     s = __builtin_amdgcn_readfirstlane(s);
     int tn = t, sn = s + 1;
@@ -375,7 +392,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
       sn = 0;
       tn += nw;
     }
-    issue(nxt, pn, tn, sn);
+    if constexpr (decltype(issue_next)::value) issue(nxt, pn, tn, sn);
     // this step's weights and epilogue inputs: consumed here, on every path (the compute below
     // skips lanes past the row's end), so no load into a register is still pending when the loop
     // comes round and the compiler's waits at the loop head stay exact
@@ -532,10 +549,21 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
     t = tn;
     s = sn;
   };
-  while (t < n_items) {
-    stage(wa, pa, wb, pb);
-    if (t >= n_items) break;
-    stage(wb, pb, wa, pa);
+  if constexpr (PRE) {
+    if (t < n_items) {
+      stage(std::false_type{}, wa, pa, wb, pb);  // the step after it is already in flight
+      while (t < n_items) {
+        stage(std::true_type{}, wb, pb, wa, pa);
+        if (t >= n_items) break;
+        stage(std::true_type{}, wa, pa, wb, pb);
+      }
+    }
+  } else {
+    while (t < n_items) {
+      stage(std::true_type{}, wa, pa, wb, pb);
+      if (t >= n_items) break;
+      stage(std::true_type{}, wb, pb, wa, pa);
+    }
   }
 }
 
