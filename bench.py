@@ -248,13 +248,14 @@ def engine_weights(model, embed, q8):
     return {"embed": embed, "lm": model.lm if not q8 else model.lm_q, "nf": model.nf, "layers": layers}
 
 
-def engine_bench(torch, hi, model, steps, T=1024, batches=(16, 32, 64), ctx=1024):
+def engine_bench(torch, hi, model, steps, T=1024, batches=(4, 8, 16, 32, 64), ctx=1024):
     """Llama-3.1-8B through the engine (hipinfer_amd.engine.DecodeStep): the prefill of a T-token
     prompt into one cache slot (embed, 32 x [RMSNorm, QKV GEMM, RoPE/cache, flash prefill, o +
     residual, gate/up + SwiGLU, down + residual GEMMs], final-norm lm_head GEMV, greedy; the
     reference's prefill, api.cu:1807-1845), timed end to end on the host clock (it ends in a
-    device->host read of the token); and the greedy decode step of B sequences on the GEMM path
-    (api.cu:1914-1940) at a context of ctx positions, captured once and replayed."""
+    device->host read of the token); and the greedy decode step of B sequences at a context of ctx
+    positions, captured once and replayed: up to 8 on the GEMV path (gate/up, down and lm_head on
+    the GEMM where the first step times it faster), more on the GEMM path (api.cu:1914-1940)."""
     from hipinfer_amd.engine import DecodeStep
     g = torch.Generator(device="cuda")
     g.manual_seed(SEED + 21)
@@ -264,7 +265,8 @@ def engine_bench(torch, hi, model, steps, T=1024, batches=(16, 32, 64), ctx=1024
     mm_params = L * sum(N * K for N, K in SHAPES.values())
     attn_flops = L * HQ * D * 4.0 * T * (T + 1) / 2  # QK^T and PV over the causal triangle
     res = {"config": f"Llama-3.1-8B engine: prefill of a {T}-token prompt (one slot, one chunk); greedy decode "
-                     f"step of B sequences on the GEMM path at ctx {ctx} (synthetic caches, hipGraph replay)"}
+                     f"step of B sequences at ctx {ctx} (synthetic caches, hipGraph replay): B <= 8 on the GEMV "
+                     "path with the per-projection GEMM choice, larger B on the GEMM path"}
     for q8 in ([False, True] if model.q8 is not None else [False]):
         tag = "int8" if q8 else "fp16"
         W = engine_weights(model, embed, q8)
@@ -288,7 +290,7 @@ def engine_bench(torch, hi, model, steps, T=1024, batches=(16, 32, 64), ctx=1024
             for k in ds.kc + ds.vc:
                 k.normal_(0.0, 1.0, generator=g)
             ds.pos.fill_(ctx - 1)
-            ds.step()  # eager: tunes the GEMM tiles of this batch size
+            ds.step()  # eager: tunes the GEMM tiles (and, up to 8 sequences, the projections' paths)
             torch.cuda.synchronize()
             gr = ds.capture()
             ds.pos.fill_(ctx - 1)
@@ -297,6 +299,7 @@ def engine_bench(torch, hi, model, steps, T=1024, batches=(16, 32, 64), ctx=1024
             wb = weight_bytes(q8)
             kv = B * L * HKV * (ctx + steps) * D * 2 * 2
             res[f"decode_B{B}_{tag}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(B / ms * 1e3, 1),
+                                        "gemm_projections": ds.small_gemm if B > 1 and not ds.gemm_path else None,
                                         "weight_GB/s": round(wb / (ms * 1e-3) / 1e9, 1),
                                         "GB/s": round((wb + kv) / (ms * 1e-3) / 1e9, 1),
                                         "pct_hbm_peak": round(100 * (wb + kv) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}

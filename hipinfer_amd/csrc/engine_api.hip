@@ -15,9 +15,14 @@
 //    state change is a kernel on the engine's stream, so a decode step is one captured hipGraph per
 //    batch size, replayed;
 //  * 1..HIPINFER_GEMV_MAX (default 8) sequences decode on the GEMV path (fused RMSNorm, fused
-//    QKV+RoPE+cache write); more on the GEMM path. The first step of a batch size runs eagerly
-//    (it tunes the GEMM tiles and sets kernel attributes, which capture cannot), the rest replay
-//    the graph captured after it.
+//    QKV+RoPE+cache write); more on the GEMM path. From 2 sequences on, the gate/up, down and
+//    lm_head projections each take whichever path the first step of that batch size times faster
+//    (the GEMM with a separate RMSNorm where the GEMV fuses it): at 5-8 rows the GEMV streams the
+//    weights twice once the rows no longer fit in LDS (Llama-3.1-8B down, K = 14336), and int8
+//    weights make it instruction-bound on the long launches. The first step of a batch size runs
+//    eagerly (it tunes the GEMM tiles and these paths, and sets kernel attributes, which capture
+//    cannot), the rest replay the graph captured after it.
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -77,6 +82,9 @@ struct Engine {
   f16x2* rope = nullptr;
   hipStream_t st = nullptr;
   std::vector<hipGraphExec_t> graphs;
+  // per batch size of 2..gemv_max sequences: the projections that run on the GEMM path (bit 0
+  // gate/up, bit 1 down, bit 2 lm_head), timed on the first eager step of that size
+  std::map<int, int> small_gemm;
   std::map<std::pair<int, int>, hipGraphExec_t> vgraphs;  // verify step per (slot, rows)
   int *v_tok = nullptr, *v_pos = nullptr, *v_out = nullptr;
   f16* v_logits = nullptr;
@@ -276,6 +284,80 @@ int moe_rows(Engine* e, const Layer& w, f16* x, f16* xn, int m) {
   return 0;
 }
 
+enum { kGuGemm = 1, kDownGemm = 2, kLmGemm = 4 };
+
+// The projections of a B-sequence decode step (2 <= B <= gemv_max) that run faster on the GEMM
+// path: each of gate/up, down and lm_head is timed both ways on scratch rows (the weights of up
+// to 8 layers in turn, so they stream from HBM as in a step), the GEMM side with the RMSNorm the
+// GEMV fuses; the GEMM must win by 3 %. HIPINFER_SMALL_GEMM=<mask> sets the choice instead.
+int tune_small_paths(Engine* e, int B, int* mask) {
+  if (const char* env = getenv("HIPINFER_SMALL_GEMM")) {
+    *mask = atoi(env) & 7;
+    return 0;
+  }
+  const Cfg& c = e->c;
+  const int H = c.hidden, I = c.inter, V = c.vocab;
+  hipStream_t s = e->st;
+  f16 *xs = nullptr, *xn = nullptr, *act = nullptr, *x2 = nullptr, *lg = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = 0;
+  const size_t hb = (size_t)B * H * 2, ib = (size_t)B * (c.moe ? 1 : I) * 2, vb = (size_t)B * V * 2;
+  if (hipMalloc(&xs, hb) != hipSuccess || hipMalloc(&xn, hb) != hipSuccess || hipMalloc(&x2, hb) != hipSuccess ||
+      hipMalloc(&act, ib) != hipSuccess || hipMalloc(&lg, vb) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+      hipEventCreate(&e1) != hipSuccess || hipMemsetAsync(xs, 0, hb, s) != hipSuccess ||
+      hipMemsetAsync(x2, 0, hb, s) != hipSuccess || hipMemsetAsync(act, 0, ib, s) != hipSuccess)
+    rc = -2;
+  const int nl = std::min<int>(c.layers, 8), reps = std::max(8, 2 * nl);
+  // microseconds per call of fn(layer), after one untimed call on each of two layers (which also
+  // tunes the GEMM tiles of these shapes)
+  auto time_us = [&](auto fn, float* us) -> int {
+    for (int l = 0; l < std::min(nl, 2); l++)
+      if (int r = fn(l)) return r;
+    if (hipEventRecord(e0, s) != hipSuccess) return -2;
+    for (int r = 0; r < reps; r++)
+      if (int rr = fn(r % nl)) return rr;
+    float ms = 0.f;
+    if (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+        hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+      return -2;
+    *us = ms * 1e3f / reps;
+    return 0;
+  };
+  auto pick = [&](int bit, auto gemv_fn, auto gemm_fn) -> int {
+    float tv = 0.f, tm = 0.f;
+    if (int r = time_us(gemv_fn, &tv)) return r;
+    if (int r = time_us(gemm_fn, &tm)) return r;
+    if (tm < 0.97f * tv) *mask |= bit;
+    return 0;
+  };
+  *mask = 0;
+  if (!rc && !c.moe) {
+    rc = pick(
+        kGuGemm, [&](int l) { return gemv(e, xs, H, e->L[l].n2, e->L[l].gu, act, I, B, 2 * I, H, 2); },
+        [&](int l) {
+          const int r = hi_rmsnorm(xs, e->L[l].n2, xn, B, H, c.eps, s);
+          return r ? r : gemm(e, xn, H, e->L[l].gu, nullptr, act, I, B, 2 * I, H, 2);
+        });
+    if (!rc)
+      rc = pick(
+          kDownGemm, [&](int l) { return gemv(e, act, I, nullptr, e->L[l].down, x2, H, B, H, I, 1); },
+          [&](int l) { return gemm(e, act, I, e->L[l].down, nullptr, x2, H, B, H, I, 1); });
+  }
+  if (!rc)
+    rc = pick(
+        kLmGemm, [&](int) { return gemv(e, xs, H, e->final_norm, e->lm, lg, V, B, V, H, 0); },
+        [&](int) {
+          const int r = hi_rmsnorm(xs, e->final_norm, xn, B, H, c.eps, s);
+          return r ? r : gemm(e, xn, H, e->lm, nullptr, lg, V, B, V, H, 0);
+        });
+  (void)hipStreamSynchronize(s);
+  for (void* p : {(void*)xs, (void*)xn, (void*)act, (void*)x2, (void*)lg})
+    if (p) (void)hipFree(p);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  return rc;
+}
+
 // One greedy decode step for slots [0, B) (api.cu:1891-1952): reads tok / pos, writes the next
 // token, advances pos, appends to the history.
 int decode_step(Engine* e, int B) {
@@ -283,6 +365,20 @@ int decode_step(Engine* e, int B) {
   const int H = c.hidden, D = c.head_dim, Hq = c.heads, Hkv = c.kv, HD = Hq * D, I = c.inter, V = c.vocab;
   const bool small = B <= e->gemv_max;
   hipStream_t s = e->st;
+  int sg = 0;  // projections of this batch size on the GEMM path (the GEMV path's are the rest)
+  if (small && B > 1) {
+    auto it = e->small_gemm.find(B);
+    if (it != e->small_gemm.end()) {
+      sg = it->second;
+    } else {
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      EN_TRY(hipStreamIsCapturing(s, &cap));
+      if (cap == hipStreamCaptureStatusNone) {  // timed once, eagerly; a capture keeps the GEMVs
+        EN_TRY(tune_small_paths(e, B, &sg));
+        e->small_gemm[B] = sg;
+      }
+    }
+  }
   EN_TRY(hi_embed(e->tok, e->embed, V, H, e->x, H, B, s));
   for (int l = 0; l < c.layers; l++) {
     const Layer& w = e->L[l];
@@ -308,15 +404,21 @@ int decode_step(Engine* e, int B) {
       continue;
     }
     if (small) {
-      EN_TRY(gemv(e, e->x, H, w.n2, w.gu, e->act, I, B, 2 * I, H, 2));
-      EN_TRY(gemv(e, e->act, I, nullptr, w.down, e->x, H, B, H, I, 1));
+      if (sg & kGuGemm) {
+        EN_TRY(hi_rmsnorm(e->x, w.n2, e->xn, B, H, c.eps, s));
+        EN_TRY(gemm(e, e->xn, H, w.gu, nullptr, e->act, I, B, 2 * I, H, 2));
+      } else {
+        EN_TRY(gemv(e, e->x, H, w.n2, w.gu, e->act, I, B, 2 * I, H, 2));
+      }
+      if (sg & kDownGemm) EN_TRY(gemm(e, e->act, I, w.down, nullptr, e->x, H, B, H, I, 1));
+      else EN_TRY(gemv(e, e->act, I, nullptr, w.down, e->x, H, B, H, I, 1));
     } else {
       EN_TRY(hi_rmsnorm(e->x, w.n2, e->xn, B, H, c.eps, s));
       EN_TRY(gemm(e, e->xn, H, w.gu, nullptr, e->act, I, B, 2 * I, H, 2));
       EN_TRY(gemm(e, e->act, I, w.down, nullptr, e->x, H, B, H, I, 1));
     }
   }
-  if (small) {
+  if (small && !(sg & kLmGemm)) {
     EN_TRY(gemv(e, e->x, H, e->final_norm, e->lm, e->logits, V, B, V, H, 0));
   } else {
     EN_TRY(hi_rmsnorm(e->x, e->final_norm, e->xn, B, H, c.eps, s));

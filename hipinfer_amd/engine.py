@@ -19,7 +19,9 @@ Prefill of T prompt tokens into slot s at positions p0.. (chunks of at most max_
 Decode step for slots 0..B-1 (tok and pos live on the device and advance there, so one captured
 hipGraph replays step after step). Up to 8 sequences take the GEMV path with RMSNorm fused into
 the projections; 9 to 64 the GEMM path (api.cu:1914-1940), whose tiles are tuned by the first,
-eager step:
+eager step. From 2 sequences on, the first step also times the gate/up, down and lm_head
+projections both ways and keeps, for each, the faster (the GEMM with a separate RMSNorm), as the
+library's engine does:
 
     x = embed[tok]
     per layer l:
@@ -36,12 +38,15 @@ The weight-file path is the library's own engine (csrc/engine_api.hip: hi_load, 
 hi_decode, hi_verify), which runs the same kernels in the same order and which hipinfer.Engine
 wraps.
 """
+import os
+
 import torch
 
 from . import hipinfer as hi
 
 GEMV_MAX = 8  # sequences per decode step on the GEMV path (the library's HIPINFER_GEMV_MAX default)
 GEMM_MAX = 64  # and on the batched-decode GEMM path
+GU_GEMM, DOWN_GEMM, LM_GEMM = 1, 2, 4  # projections of a GEMV-path step that run on the GEMM
 
 
 class DecodeStep:
@@ -50,12 +55,17 @@ class DecodeStep:
     "layers": [{"qkv", "o", "gate_up", "down": [N, K] fp16 or (int8, scales); "bqkv": bias or None;
     "n1", "n2": [H]}]} with gate/up rows interleaved in groups of 16 (export.py:97-101).
     B: cache slots = sequences per decode step (1..64); max_prefill: rows per prefill chunk (0: no
-    prefill buffers)."""
+    prefill buffers); small_gemm: for 2..8 sequences, the mask of projections (GU_GEMM, DOWN_GEMM,
+    LM_GEMM) to run on the GEMM path, or None to time them on the first eager step (the
+    HIPINFER_SMALL_GEMM environment variable, when set, gives the mask instead)."""
 
-    def __init__(self, cfg, weights, B, max_seq, max_prefill=0):
+    def __init__(self, cfg, weights, B, max_seq, max_prefill=0, small_gemm=None):
         assert 1 <= B <= GEMM_MAX, f"1..{GEMM_MAX} sequences per decode step"
         self.c, self.w, self.B, self.max_seq = dict(cfg), weights, B, max_seq
         self.gemm_path = B > GEMV_MAX
+        if small_gemm is None and os.environ.get("HIPINFER_SMALL_GEMM"):
+            small_gemm = int(os.environ["HIPINFER_SMALL_GEMM"]) & 7
+        self.small_gemm = 0 if (B == 1 or self.gemm_path) else small_gemm  # None: not timed yet
         H, Hq, Hkv, D, I, V, L = (cfg[k] for k in ("H", "Hq", "Hkv", "D", "I", "V", "L"))
         self.qkv_dim = (Hq + 2 * Hkv) * D
         dev = "cuda"
@@ -65,8 +75,8 @@ class DecodeStep:
         self.att = torch.zeros(B, Hq * D, dtype=f16, device=dev)
         self.act = torch.zeros(B, I, dtype=f16, device=dev)
         self.logits = torch.zeros(B, V, dtype=f16, device=dev)
+        self.xn = torch.zeros(B, H, dtype=f16, device=dev)
         if self.gemm_path:
-            self.xn = torch.zeros(B, H, dtype=f16, device=dev)
             self.qkv = torch.zeros(B, self.qkv_dim, dtype=f16, device=dev)
         self.kc = [torch.zeros(B, Hkv, max_seq, D, dtype=f16, device=dev) for _ in range(L)]
         self.vc = [torch.zeros_like(k) for k in self.kc]
@@ -99,11 +109,58 @@ class DecodeStep:
         Wd, sd = self._ws(ly["down"])
         hi.gemm(act, Wd, out=x, epi=1, scales=sd)
 
+    def _tune_small_paths(self, eps):
+        """Time gate/up, down and lm_head on the GEMV path and on the GEMM path (with the RMSNorm
+        the GEMV fuses), on scratch rows and the weights of up to 8 layers in turn; keep the GEMM
+        where it is at least 3 % faster."""
+        w, B = self.w, self.B
+        lys = w["layers"][:8]
+        reps = max(8, 2 * len(lys))
+        xs, x2 = torch.zeros_like(self.x), torch.zeros_like(self.x)
+        xn, act, lg = torch.zeros_like(self.xn), torch.zeros_like(self.act), torch.zeros_like(self.logits)
+
+        def time_us(fn, n):
+            for i in range(min(n, 2)):  # untimed: also tunes the GEMM tiles of these shapes
+                fn(i)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for r in range(reps):
+                fn(r % n)
+            e1.record()
+            e1.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / reps
+
+        def pick(bit, gemv_fn, gemm_fn, n):
+            return bit if time_us(gemm_fn, n) < 0.97 * time_us(gemv_fn, n) else 0
+
+        def gu_gemm(i):
+            hi.rmsnorm(xs, lys[i]["n2"], eps, out=xn)
+            Wg, sg = self._ws(lys[i]["gate_up"])
+            hi.gemm(xn, Wg, out=act, epi=2, scales=sg)
+
+        def lm_gemm(i):
+            hi.rmsnorm(xs, w["nf"], eps, out=xn)
+            hi.gemm(xn, Wl, out=lg, scales=sl)
+
+        Wl, sl = self._ws(w["lm"])
+        mask = pick(GU_GEMM, lambda i: hi.gemv(xs, self._ws(lys[i]["gate_up"])[0], out=act, normw=lys[i]["n2"],
+                                               eps=eps, epi=2, scales=self._ws(lys[i]["gate_up"])[1]),
+                    gu_gemm, len(lys))
+        mask |= pick(DOWN_GEMM, lambda i: hi.gemv(act, self._ws(lys[i]["down"])[0], out=x2, epi=1,
+                                                  scales=self._ws(lys[i]["down"])[1]),
+                     lambda i: hi.gemm(act, self._ws(lys[i]["down"])[0], out=x2, epi=1,
+                                       scales=self._ws(lys[i]["down"])[1]), len(lys))
+        mask |= pick(LM_GEMM, lambda i: hi.gemv(xs, Wl, out=lg, normw=w["nf"], eps=eps, scales=sl), lm_gemm, 1)
+        return mask
+
     def step(self):
         """One token for every slot: reads tok / pos, writes the next tok, advances pos."""
         c, w = self.c, self.w
         eps = float(c.get("eps", 1e-5))
         Hq, Hkv, D = c["Hq"], c["Hkv"], c["D"]
+        if self.small_gemm is None:  # a capture before the first eager step keeps the GEMVs
+            self.small_gemm = 0 if torch.cuda.is_current_stream_capturing() else self._tune_small_paths(eps)
+        sg = self.small_gemm
         hi.embed(self.tok, w["embed"], out=self.x)
         for l, ly in enumerate(w["layers"]):
             Wq, sq = self._ws(ly["qkv"])
@@ -123,12 +180,19 @@ class DecodeStep:
                 self._mlp_gemm(ly, self.x, self.xn, self.act, eps)
             else:
                 hi.gemv(self.att, Wo, out=self.x, epi=1, scales=so)
-                Wg, sg = self._ws(ly["gate_up"])
-                hi.gemv(self.x, Wg, out=self.act, normw=ly["n2"], eps=eps, epi=2, scales=sg)
+                Wg, s_g = self._ws(ly["gate_up"])
+                if sg & GU_GEMM:
+                    hi.rmsnorm(self.x, ly["n2"], eps, out=self.xn)
+                    hi.gemm(self.xn, Wg, out=self.act, epi=2, scales=s_g)
+                else:
+                    hi.gemv(self.x, Wg, out=self.act, normw=ly["n2"], eps=eps, epi=2, scales=s_g)
                 Wd, sd = self._ws(ly["down"])
-                hi.gemv(self.act, Wd, out=self.x, epi=1, scales=sd)
+                if sg & DOWN_GEMM:
+                    hi.gemm(self.act, Wd, out=self.x, epi=1, scales=sd)
+                else:
+                    hi.gemv(self.act, Wd, out=self.x, epi=1, scales=sd)
         Wl, sl = self._ws(w["lm"])
-        if self.gemm_path:
+        if self.gemm_path or sg & LM_GEMM:
             hi.rmsnorm(self.x, w["nf"], eps, out=self.xn)
             hi.gemm(self.xn, Wl, out=self.logits, scales=sl)
         else:
@@ -137,8 +201,9 @@ class DecodeStep:
         self.pos.add_(1)
 
     def capture(self):
-        """The step as a hipGraph (replay it to decode; tok / pos advance on the device). On the
-        GEMM path, run one eager step first: tile tuning does not run under capture."""
+        """The step as a hipGraph (replay it to decode; tok / pos advance on the device). Run one
+        eager step first: neither the GEMM tile tuning nor the timing of the 2-8-sequence paths runs
+        under capture (a capture before it keeps those projections on the GEMV)."""
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             self.step()

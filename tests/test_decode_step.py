@@ -85,15 +85,18 @@ def oracle_step(O, c, Wd, tok, pos, kc, vc, cs):
     return logits, O.argmax(logits)
 
 
+@pytest.mark.parametrize("mask", [None, 7, 2], ids=["timed_paths", "gemm_gu_down_lm", "gemm_down"])
 @pytest.mark.parametrize("q8", [False, True], ids=["fp16", "int8"])
-def test_decode_step_vs_oracle_chain(hi, O, q8):
+def test_decode_step_vs_oracle_chain(hi, O, q8, mask):
+    """mask: the projections a 2-sequence step runs on the GEMM path (engine.GU_GEMM | DOWN_GEMM |
+    LM_GEMM), or None for the choice the first step times; every choice must match the oracle."""
     import torch
     from hipinfer_amd.engine import DecodeStep
     r = rng(800 + q8)
     c = CFG
     B, S = 2, 64
     Wd = to_device(hi, make_weights(r, c), q8)
-    ds = DecodeStep(c, Wd, B, S)
+    ds = DecodeStep(c, Wd, B, S, small_gemm=mask)
     p0 = np.array([5, 17], np.int32)
     kc = [r.standard_normal((B, c["Hkv"], S, c["D"])).astype(np.float16) for _ in range(c["L"])]
     vc = [r.standard_normal((B, c["Hkv"], S, c["D"])).astype(np.float16) for _ in range(c["L"])]

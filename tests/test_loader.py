@@ -149,7 +149,7 @@ def clear(lg, tol=5e-2):
 
 
 @pytest.mark.parametrize("kind", ["dense_bias", "tied", "int8", "moe"])
-def test_engine_from_weight_file_vs_oracle_chain(hi, O, tmp_path, kind):
+def test_engine_from_weight_file_vs_oracle_chain(hi, O, tmp_path, kind, monkeypatch):
     from hipinfer_amd.weights import write_weights
     r = rng(1500 + ["dense_bias", "tied", "int8", "moe"].index(kind))
     cfg, W, ov = make_model(O, r, kind)
@@ -190,6 +190,10 @@ def test_engine_from_weight_file_vs_oracle_chain(hi, O, tmp_path, kind):
         e.prefill(1, Bp)
         ref_lg1, ref_tok1 = o_prefill(O, ov, Bp, 0, 1, kc, vc, cs)
         e.set_state([t, ref_tok1], [pos, 10])
+        # the two-slot step's gate/up, down and lm_head: the timed choice (dense_bias, moe), or all
+        # three forced onto the GEMM path (tied, int8)
+        if kind in ("tied", "int8"):
+            monkeypatch.setenv("HIPINFER_SMALL_GEMM", "7")
         e.decode(2, 1)
         ref_lg, ref_t = o_decode(O, ov, [t, ref_tok1], [pos, 10], kc, vc, cs)
         check(f"{kind} two-slot decode logits", host(e.logits(2)), ref_lg, tol, tol)
