@@ -589,9 +589,13 @@ int gemv_launch(const GemvArgs& a, hipStream_t s) {
   // fuller blocks: 8 items in flight per CU suffice, and among shapes of equal load the one with
   // the fewest blocks wins (each block stages the activation row once; measured on MI355X at
   // Llama-3.1-8B shapes: fp16 down 19.14-19.25 against 19.25-19.26 us, int8 lm_head 78.5-78.7
-  // against 79.6-79.7, the fp16 token 2504 against 2510 us). Other launches keep 16 in flight.
-  const bool lean = MR == 1 && (EPI == 1 || (EPI == 0 && WF != WF_F16));
-  const int need = std::min(std::min(per_cu, lean ? 8 : 16), bpc * kGemvWaves);  // items in flight per CU, at least
+  // against 79.6-79.7, the fp16 token 2504 against 2510 us). The one-row int8 QKV launch does the
+  // same with 6 in flight, so that each wave streams two row pairs instead of requesting all of
+  // its CU's share at once (7.08 against 7.43 us; the fp16 one ran slower that way, 10.30 against
+  // 10.12). Other launches keep 16 in flight.
+  const bool qkv8 = MR == 1 && EPI == 3 && WF != WF_F16;
+  const bool lean = MR == 1 && (EPI == 1 || qkv8 || (EPI == 0 && WF != WF_F16));
+  const int need = std::min(std::min(per_cu, qkv8 ? 6 : lean ? 8 : 16), bpc * kGemvWaves);  // items in flight per CU, at least
   int grid = 1, ipb = 1;
   long best_load = -1;
   int best_fly = 0;
