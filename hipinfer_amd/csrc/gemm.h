@@ -67,14 +67,6 @@ struct GemmArgs {
 };
 
 constexpr int kGemmBK = 64;
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// Wait until at most N vector-memory operations (global loads, LDS DMA) are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 // Wait until every LDS read of this wave has returned.
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 // Workgroup barrier without a memory fence (a fence would drain every in-flight LDS DMA); the

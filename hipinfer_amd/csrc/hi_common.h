@@ -55,6 +55,14 @@ int hi_blocks_per_cu(const void* fn, int block, size_t lds);
 int hi_gemv_max_rows();
 
 // ------------------------------------------------------------------ device helpers
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Wait until at most N vector-memory operations (global loads, LDS DMA) are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 // DPP lane moves with compile-time controls (gfx9 encodings): quad_perm, row_half_mirror, row_mirror.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {

@@ -4,68 +4,139 @@
 // hi_flash_prefill_lse; api.cu:594-623, kernels.cuh:1160-1329, ctypes hipinfer.py:171-202).
 //
 // Flash prefill for gfx950 (D = 64 or 128):
-//  * block = 128 query rows of one query head, 4 waves of 32 rows; the wave's Q rows stay in
+//  * block = 32 RG query rows of one query head and 2 RG waves: the waves of row group g (g and
+//    g + RG) share its 32 rows and split every 64-key tile, keys 0..31 and 32..63, each with its
+//    own online-softmax state; the pair merges (m, l, O) through LDS at the end. Two waves per
+//    SIMD let one wave's softmax run beside the other's matrix work. The wave's Q rows stay in
 //    registers as v_mfma_f32_32x32x16_f16 operands for the whole kernel;
-//  * 64-key K/V tiles of the head's cache rows are loaded once per block (global -> registers ->
-//    LDS, the next tile's loads in flight while the current one is computed). K is stored with its
-//    16-byte chunks XOR-swizzled by the key so fragment reads are conflict-free; V is stored
-//    transposed (V^T[d][key]), because the P.V product contracts over keys;
-//  * S^T = K Q^T: with the K fragment as first operand each lane ends with 32 keys of ONE query
-//    row (16 keys x 2 halves of the tile, split between lanes l and l + 32), so the row max and sum
-//    of the online softmax are the lane's own values plus one exchange with lane l ^ 32;
+//  * 64-key K/V tiles of the head's cache rows go straight from global memory into LDS by buffer
+//    DMA (no register staging), two LDS stages: tile j + 1 streams in while tile j is computed,
+//    one barrier per tile. Both tiles keep the cache's row-major order with their 16-byte chunks
+//    XOR-swizzled by the key; the swizzle is applied to the DMA's per-lane source address, since
+//    a DMA instruction writes 64 consecutive 16-byte LDS slots;
+//  * S^T = K Q^T over the wave's 32 keys: with the K fragment as first operand each lane ends with
+//    16 keys of ONE query row (split between lanes l and l + 32), so the row max and sum of the
+//    online softmax are the lane's own values plus one exchange with lane l ^ 32;
 //  * logits are scaled by log2(e) / sqrt(D) and the softmax runs in base 2 (the reference's
 //    log2-domain form, kernels.cuh:1236-1262); P is rounded to fp16 for P.V, the row sum l keeps
-//    fp32 p, as the reference does;
+//    fp32 p, as the reference does. exp2 is the hardware's v_exp_f32, whose results below 2^-126
+//    flush to zero: such p round to fp16 zero anyway and vanish against l >= 1 in fp32. O is
+//    rescaled only when some row's running max moved;
 //  * O^T += V^T P^T: the P registers of a lane are already a B fragment of the next product once
 //    the key order inside each 16-key step is permuted identically for P and V^T (lane half fk
-//    takes keys 4 fk + 0..3 and 8 + 4 fk + 0..3), so P never goes through LDS; O^T keeps the
-//    lane -> query row map, so the per-row rescale by exp2(m_old - m_new) is per lane;
-//  * causal mask on absolute positions (row t at p0 + t sees keys 0..p0+t); a wave skips tiles
-//    that lie wholly above its rows' diagonal; cache rows past the block's last key read as zeros.
+//    takes keys 4 fk + 0..3 and 8 + 4 fk + 0..3), so P never goes through LDS. The V^T fragments
+//    come from the row-major V tile through ds_read_tr16_b64, which transposes 4 keys x 16 d
+//    blocks within each 16-lane group; O^T keeps the lane -> query row map, so the per-row
+//    rescale by exp2(m_old - m_new) is per lane;
+//  * causal mask on absolute positions (row t at p0 + t sees keys 0..p0+t); a wave skips key
+//    halves that lie wholly above its rows' diagonal and drops the mask on halves wholly below
+//    it; cache rows past the block's last key read as zeros (the DMA's buffer range ends there);
+//  * blocks run the longest query tiles (the most keys) first, across all heads.
 #include "hi_common.h"
 
 namespace {
 
-constexpr int kFpWaves = 4;
-constexpr int kFpBQ = 32 * kFpWaves;  // query rows per block
+constexpr int kFpRG = 4;              // 32-row groups per block (2 waves each)
+constexpr int kFpBQ = 32 * kFpRG;     // query rows per block
 constexpr int kFpBKV = 64;            // keys per tile
-constexpr int kVtStride = kFpBKV + 4;  // halves per V^T row: 136 bytes keeps 8-byte reads aligned
+constexpr int kFpStages = 2;          // LDS stages of K/V tiles
 
-// Slot of 16-byte chunk c of key r in the K tile (D / 8 chunks per key): the XOR term spreads the
-// 16 keys one 128-bit read serves per cycle over all 64 banks.
+// XOR term of key r's 16-byte chunks in the K tile: the 16 keys (D = 128) or 8 key pairs (D = 64)
+// that one 128-bit fragment read serves per cycle land on distinct banks.
 template <int D>
-__device__ __forceinline__ int k_slot(int r, int c) {
-  if constexpr (D == 128) return r * 16 + (c ^ (r & 15));
-  else return r * 8 + (c ^ ((r >> 1) & 7));
+__device__ __forceinline__ int k_swz(int r) {
+  if constexpr (D == 128) return r & 15;
+  else return (r >> 1) & 7;
+}
+// XOR term of key r's chunks in the V tile. A transpose read covers keys r..r+3 (r % 4 == 0) at
+// 4 consecutive chunks per 32 lanes and 2 per 16 lanes; the terms 0, 6, 12, 10 (D = 128) or 0, 6,
+// 4, 2 (D = 64) for r % 4 = 0..3 move those chunks to distinct banks at either width.
+template <int D>
+__device__ __forceinline__ int v_swz(int r) {
+  const int a = r & 3;
+  return ((2 * a) ^ (4 * a)) & (D / 8 - 1);
 }
 
 template <int D>
-struct FpSmem {
+struct FpStage {
   u32x4 k[kFpBKV * D / 8];
-  f16 vt[D * kVtStride];
+  u32x4 v[kFpBKV * D / 8];
+};
+// The O^T accumulators the second wave of each row group hands to the first at the end (in the
+// stages' LDS).
+template <int D, int RG>
+struct FpMerge {
+  f32x16 o[RG][D / 32][64];
 };
 
-template <int D>
-__global__ void __launch_bounds__(64 * kFpWaves)
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// The two builtins below sit in the device pass only: in this kernel's host pass they made the
+// compiler drop the kernel's launch stub without a diagnostic (an undefined symbol at load).
+// 16-byte buffer DMA of each lane's chunk at byte offset voff into LDS slot lane of `lds`.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voff, 0, 0, 0);
+#endif
+}
+// ds_read_tr16_b64 at LDS address p: within each 16-lane group, lane i receives element i % 4 of
+// the 4 halves lane 4 e + i / 4 addresses, as its element e.
+__device__ __forceinline__ f16x4 lds_read_tr16(const f16* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p));
+#else
+  return f16x4{};
+#endif
+}
+
+template <int D, int RG>
+__global__ void __launch_bounds__(128 * RG)
     flash_prefill_kernel(const f16* __restrict__ q, int64_t ldq, const f16* __restrict__ kc,
                          const f16* __restrict__ vc, int max_seq, f16* __restrict__ out, int64_t ldo, int T, int p0,
                          int Hq, int Hkv, float scale_log2, float* __restrict__ lse) {
-  constexpr int CPR = D / 8;                    // 16-byte chunks per key row
-  constexpr int NT = 64 * kFpWaves;
-  constexpr int LPT = kFpBKV * CPR / NT;        // chunks of K (and of V) each thread loads per tile
-  constexpr int DT = D / 32;                    // 32-row output tiles of O^T
-  static_assert(LPT * NT == kFpBKV * CPR, "tile load split");
-  __shared__ FpSmem<D> sm;
+  constexpr int NW = 2 * RG, BQ = 32 * RG;
+  constexpr int CPR = D / 8;                   // 16-byte chunks per key row
+  constexpr int IPW = kFpBKV * CPR / 64 / NW;  // DMA instructions per wave per tile and operand
+  constexpr int DT = D / 32;                   // 32-row output tiles of O^T
+  static_assert(IPW * 64 * NW == kFpBKV * CPR, "tile DMA split");
+  static_assert(sizeof(FpMerge<D, RG>) <= sizeof(FpStage<D>) * kFpStages, "merge fits the stages");
+  __shared__ FpStage<D> sm[kFpStages];
+  __shared__ float ml[2][RG][64];  // the second waves' m and l
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rg = wave % RG, kh = wave / RG;     // row group, key half
   const int fr = lane & 31, fk = lane >> 5;
-  const int q0 = blockIdx.x * kFpBQ, h = blockIdx.y, hk = h / (Hq / Hkv);
-  const int qw = q0 + wave * 32;                // this wave's first query row
+  // grid (Hq, query tiles), dispatched x first: all heads' longest query tile first; block x runs
+  // on XCD x % 8, which takes a contiguous range of query heads (those sharing a KV head)
+  const int q0 = (gridDim.y - 1 - blockIdx.y) * BQ;
+  const int h = Hq % 8 ? blockIdx.x : (blockIdx.x % 8) * (Hq / 8) + blockIdx.x / 8, hk = h / (Hq / Hkv);
+  const int qw = q0 + rg * 32;                  // this wave's first query row
   const int qi = qw + fr;                       // this lane's query row
   const int qpos = p0 + qi;
-  const int kv_end = p0 + min(q0 + kFpBQ, T);   // keys any row of the block can see
-  const f16* Kh = kc + (int64_t)hk * max_seq * D;
-  const f16* Vh = vc + (int64_t)hk * max_seq * D;
+  const int kv_end = p0 + min(q0 + BQ, T);      // keys any row of the block can see
+  // the head's cache rows 0..kv_end-1: loads past them return zeros
+  const __amdgpu_buffer_rsrc_t k_rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<f16*>(kc + (int64_t)hk * max_seq * D), (short)0, kv_end * D * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<f16*>(vc + (int64_t)hk * max_seq * D), (short)0, kv_end * D * 2, 0x00020000);
+
+  // DMA instruction i of this wave fills slots (wave IPW + i) * 64 + lane of a tile: slot s holds
+  // key s / CPR, physical chunk s % CPR, i.e. logical chunk (s % CPR) ^ swz(key)
+  int koff[IPW], voff[IPW];
+#pragma unroll
+  for (int i = 0; i < IPW; i++) {
+    const int s = (wave * IPW + i) * 64 + lane, r = s / CPR, p = s % CPR;
+    koff[i] = (r * D + 8 * (p ^ k_swz<D>(r))) * 2;
+    voff[i] = (r * D + 8 * (p ^ v_swz<D>(r))) * 2;
+  }
+  auto issue = [&](int j0, int st) {
+#pragma unroll
+    for (int i = 0; i < IPW; i++) {
+      lds_dma16(k_rs, &sm[st].k[(wave * IPW + i) * 64], koff[i] + j0 * D * 2);
+      lds_dma16(v_rs, &sm[st].v[(wave * IPW + i) * 64], voff[i] + j0 * D * 2);
+    }
+  };
+  issue(0, 0);
 
   // this lane's Q fragments: row qi, d = 16 ks + 8 fk + 0..7 (zero past T)
   f16x8 qf[D / 16];
@@ -76,16 +147,15 @@ __global__ void __launch_bounds__(64 * kFpWaves)
     qf[ks] = __builtin_bit_cast(f16x8, v);
   }
 
-  u32x4 kreg[LPT], vreg[LPT];
-  auto gload = [&](int j0) {
-#pragma unroll
-    for (int i = 0; i < LPT; i++) {
-      const int ci = tid + i * NT, r = ci / CPR, c = ci % CPR;
-      const bool ok = j0 + r < kv_end;
-      kreg[i] = ok ? *reinterpret_cast<const u32x4*>(Kh + (int64_t)(j0 + r) * D + 8 * c) : u32x4{0u, 0u, 0u, 0u};
-      vreg[i] = ok ? *reinterpret_cast<const u32x4*>(Vh + (int64_t)(j0 + r) * D + 8 * c) : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
+  // transpose reads of V: lane j of each 16-lane group g reads 4 d of key 4 (g / 2) + j / 4 (+ the
+  // step's key base), d = 16 (g % 2) + 4 (j % 4) (+ the output tile's d base); the group's lane i
+  // then holds d = 16 (g % 2) + i of those 4 keys. Keys of one read are 4-aligned, so the swizzle
+  // term is the lane's own.
+  const int vr = 4 * fk + ((lane & 15) >> 2);                  // key within a 16-key step
+  const int vc0 = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);   // logical chunk within a 32-d tile
+  const int vsw = v_swz<D>(vr), vh = 4 * (lane & 1);           // swizzle term, half within the chunk
+  const int kr = 32 * kh + fr;                                 // K row of this lane's fragments
+  const int ksw = k_swz<D>(kr);
 
   float m_i = -__builtin_huge_valf(), l_i = 0.f;
   f32x16 o[DT];
@@ -94,96 +164,109 @@ __global__ void __launch_bounds__(64 * kFpWaves)
 #pragma unroll
     for (int e = 0; e < 16; e++) o[dt][e] = 0.f;
 
-  gload(0);
-  for (int j0 = 0; j0 < kv_end; j0 += kFpBKV) {
-    __syncthreads();  // every wave is done with the previous tile
-#pragma unroll
-    for (int i = 0; i < LPT; i++) {
-      const int ci = tid + i * NT, r = ci / CPR, c = ci % CPR;
-      sm.k[k_slot<D>(r, c)] = kreg[i];
-      const f16x8 v = __builtin_bit_cast(f16x8, vreg[i]);
-#pragma unroll
-      for (int e = 0; e < 8; e++) sm.vt[(8 * c + e) * kVtStride + r] = v[e];
-    }
-    __syncthreads();
-    if (j0 + kFpBKV < kv_end) gload(j0 + kFpBKV);
-    if (j0 > p0 + qw + 31) continue;  // the whole tile is above this wave's diagonal
+  int st = 0;
+  for (int j0 = 0; j0 < kv_end; j0 += kFpBKV, st ^= 1) {
+    wait_vmcnt<0>();  // this wave's share of tile j0 is in LDS
+    __syncthreads();  // every share is, and every wave is done with the other stage
+    if (j0 + kFpBKV < kv_end) issue(j0 + kFpBKV, st ^ 1);
+    const int k0 = j0 + 32 * kh;                    // this wave's first key
+    if (k0 > p0 + qw + 31 || k0 >= kv_end) continue;  // every key of the half is masked for every row
+    const bool full = k0 + 31 <= p0 + qw && k0 + 32 <= kv_end;  // no key of the half is masked
+    const u32x4* ks_ = sm[st].k;
+    const f16* vs_ = reinterpret_cast<const f16*>(sm[st].v);
 
-    // ---- S^T = K Q^T: two 32-key halves; lane (row fr, half fk) gets keys 8 g + 4 fk + e
-    f32x16 s[2];
+    // ---- S^T = K Q^T over the wave's 32 keys; lane (row fr, half fk) gets keys 8 g + 4 fk + e
+    f32x16 s;
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
+    for (int e = 0; e < 16; e++) s[e] = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; e++) s[kt][e] = 0.f;
-      const int r = kt * 32 + fr;
-#pragma unroll
-      for (int ks = 0; ks < D / 16; ks++) {
-        const f16x8 kf = __builtin_bit_cast(f16x8, sm.k[k_slot<D>(r, 2 * ks + fk)]);
-        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[kt], 0, 0, 0);
-      }
+    for (int ks = 0; ks < D / 16; ks++) {
+      const f16x8 kf = __builtin_bit_cast(f16x8, ks_[kr * CPR + ((2 * ks + fk) ^ ksw)]);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s, 0, 0, 0);
     }
-    // ---- online softmax of row qi over this tile (base 2)
+    // ---- online softmax of row qi over these keys (base 2)
     float mx = -__builtin_huge_valf();
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
+    if (full) {
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const int kp = j0 + kt * 32 + 8 * (e >> 2) + 4 * fk + (e & 3);
-        const float v = (kp <= qpos && kp < kv_end) ? s[kt][e] * scale_log2 : -__builtin_huge_valf();
-        s[kt][e] = v;
+        s[e] *= scale_log2;
+        mx = fmaxf(mx, s[e]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int kp = k0 + 8 * (e >> 2) + 4 * fk + (e & 3);
+        const float v = (kp <= qpos && kp < kv_end) ? s[e] * scale_log2 : -__builtin_huge_valf();
+        s[e] = v;
         mx = fmaxf(mx, v);
       }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m_i, mx);
-    const float alpha = m_new == -__builtin_huge_valf() ? 1.f : exp2f(m_i - m_new);
+    // m_new is -inf only for a row that has seen no key yet (a row past T, or one whose first
+    // key lies in the other half): then every p and alpha is taken as 0 and 1
+    const float m_use = m_new == -__builtin_huge_valf() ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
     float sum = 0.f;
-    f16x8 pf[2][2];
+    f16x8 pf[2];
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const float p = s[kt][e] == -__builtin_huge_valf() ? 0.f : exp2f(s[kt][e] - m_new);
-        sum += p;
-        pf[kt][e >> 3][e & 7] = (f16)p;
-      }
+    for (int e = 0; e < 16; e++) {
+      const float p = __builtin_amdgcn_exp2f(s[e] - m_use);
+      sum += p;
+      pf[e >> 3][e & 7] = (f16)p;
+    }
     sum += __shfl_xor(sum, 32);
     l_i = l_i * alpha + sum;
     m_i = m_new;
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[dt][e] *= alpha;
+    }
+    // ---- O^T += V^T P^T; step ss: lane half fk holds keys 16 ss + 4 fk + 0..3 and
+    //      16 ss + 8 + 4 fk + 0..3 of the wave's half, in P's registers and in the V^T reads alike
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) o[dt][e] *= alpha;
-    // ---- O^T += V^T P^T; step st of half kt: lane half fk holds keys 16 st + 4 fk + 0..3 and
-    //      16 st + 8 + 4 fk + 0..3 of that half, in P's registers and in the V^T reads alike
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++) {
-      const f16* vrow = sm.vt + (dt * 32 + fr) * kVtStride;
-#pragma unroll
-      for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int st = 0; st < 2; st++) {
-          const int kk = kt * 32 + 16 * st + 4 * fk;
-          const f16x4 a = *reinterpret_cast<const f16x4*>(vrow + kk);
-          const f16x4 b = *reinterpret_cast<const f16x4*>(vrow + kk + 8);
-          const f16x8 vf = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kt][st], o[dt], 0, 0, 0);
-        }
-    }
+      for (int ss = 0; ss < 2; ss++) {
+        const int key = 32 * kh + 16 * ss + vr;
+        const f16* pa = vs_ + key * D + 8 * ((4 * dt + vc0) ^ vsw) + vh;
+        const f16x4 fa = lds_read_tr16(pa), fb = lds_read_tr16(pa + 8 * D);  // key + 8: same swizzle term
+        const f16x8 vf = {fa[0], fa[1], fa[2], fa[3], fb[0], fb[1], fb[2], fb[3]};
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ss], o[dt], 0, 0, 0);
+      }
   }
 
-  if (qi >= T) return;
-  if (lse && fk == 0) lse[(int64_t)h * T + qi] = m_i + log2f(l_i);
-  const float inv = 1.f / l_i;
+  // ---- merge the two key halves of each row group: the second wave hands (m, l, O) over
+  __syncthreads();  // every wave is done with the stages (no DMA is in flight after the last tile)
+  FpMerge<D, RG>& mg = *reinterpret_cast<FpMerge<D, RG>*>(sm);
+  if (kh == 1) {
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) mg.o[rg][dt][lane] = o[dt];
+    ml[0][rg][lane] = m_i;
+    ml[1][rg][lane] = l_i;
+  }
+  __syncthreads();
+  if (kh == 1 || qi >= T) return;
+  const float m1 = ml[0][rg][lane], l1 = ml[1][rg][lane];
+  const float m = fmaxf(m_i, m1);  // finite: key 0 is visible to every row
+  const float a0 = __builtin_amdgcn_exp2f(m_i - m), a1 = __builtin_amdgcn_exp2f(m1 - m);
+  const float l = l_i * a0 + l1 * a1;
+  if (lse && fk == 0) lse[(int64_t)h * T + qi] = m + log2f(l);
+  const float inv = 1.f / l;
   f16* orow = out + (int64_t)qi * ldo + h * D;
 #pragma unroll
-  for (int dt = 0; dt < DT; dt++)
+  for (int dt = 0; dt < DT; dt++) {
+    const f32x16 o1 = mg.o[rg][dt][lane];
 #pragma unroll
     for (int g = 0; g < 4; g++) {
       f16x4 v;
 #pragma unroll
-      for (int e = 0; e < 4; e++) v[e] = (f16)(o[dt][4 * g + e] * inv);
+      for (int e = 0; e < 4; e++) v[e] = (f16)((o[dt][4 * g + e] * a0 + o1[4 * g + e] * a1) * inv);
       *reinterpret_cast<f16x4*>(orow + dt * 32 + 8 * g + 4 * fk) = v;
     }
+  }
 }
 
 // One qkv row per block: q heads rotated in place, rotated k and raw v to the cache.
@@ -259,13 +342,14 @@ int flash_prefill(const void* q, int ldq, const void* kc, const void* vc, int ma
   if (!aligned(kc, 16) || !aligned(vc, 16)) HI_FAIL("%s: kc / vc must be 16-byte aligned", who);
   if (!aligned(out, 8) || ldo % 4 || ldo < Hq * D) HI_FAIL("%s: out must be 8-byte aligned, ldo %% 4 == 0, ldo >= Hq*D", who);
   const float scale_log2 = 1.4426950408889634f / sqrtf((float)D);
-  const dim3 grid((T + kFpBQ - 1) / kFpBQ, Hq);
+  if ((T + kFpBQ - 1) / kFpBQ > 65535) HI_FAIL("%s: T=%d exceeds %d query rows", who, T, 65535 * kFpBQ);
+  const dim3 grid(Hq, (T + kFpBQ - 1) / kFpBQ);
   const hipStream_t s = (hipStream_t)stream;
   if (D == 128)
-    hipLaunchKernelGGL(flash_prefill_kernel<128>, grid, dim3(64 * kFpWaves), 0, s, (const f16*)q, (int64_t)ldq,
+    hipLaunchKernelGGL((flash_prefill_kernel<128, kFpRG>), grid, dim3(128 * kFpRG), 0, s, (const f16*)q, (int64_t)ldq,
                        (const f16*)kc, (const f16*)vc, max_seq, (f16*)out, (int64_t)ldo, T, p0, Hq, Hkv, scale_log2, lse);
   else
-    hipLaunchKernelGGL(flash_prefill_kernel<64>, grid, dim3(64 * kFpWaves), 0, s, (const f16*)q, (int64_t)ldq,
+    hipLaunchKernelGGL((flash_prefill_kernel<64, kFpRG>), grid, dim3(128 * kFpRG), 0, s, (const f16*)q, (int64_t)ldq,
                        (const f16*)kc, (const f16*)vc, max_seq, (f16*)out, (int64_t)ldo, T, p0, Hq, Hkv, scale_log2, lse);
   HI_TRY(hipGetLastError());
   return 0;
