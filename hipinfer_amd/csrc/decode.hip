@@ -350,6 +350,7 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float best, int bi
 }
 
 constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxLoads = 16;
 __global__ void __launch_bounds__(kArgmaxThreads) argmax_kernel(const f16* __restrict__ logits, int V,
                                                                 int* __restrict__ tok_out) {
   __shared__ float bv[kArgmaxThreads / 64];
@@ -358,22 +359,58 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_kernel(const f16* __res
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float best = -__builtin_huge_valf();
   int idx = 0;
-  if (((uintptr_t)row & 15) == 0) {  // 8 logits per 16-byte load, then the tail
+  auto scan = [&](int i) {  // one logit by the exact rule
+    const float v = (float)row[i];
+    if (argmax_better(v, i, best, idx)) { best = v; idx = i; }
+  };
+  if (((uintptr_t)row & 15) == 0) {  // 8 logits per 16-byte chunk, then the tail
+    // Thread t takes chunks t, t + kArgmaxThreads, ..., issuing up to kArgmaxLoads loads before
+    // looking at any (a 128K vocabulary row in one round trip). Per chunk, packed fp16 max and
+    // add only: the chunk's max against the thread's best (strictly greater replaces it, so the
+    // thread keeps its lowest chunk holding its max), and a running sum that turns NaN if any
+    // logit is NaN (or, harmlessly, if +inf and -inf overflow meet). Afterwards the thread finds
+    // its index inside that chunk (reloaded from L2; keeping its words in registers measured no
+    // faster); a thread whose sum is NaN rescans its chunks by the exact rule.
     const int V8 = V / 8;
-    for (int c = tid; c < V8; c += kArgmaxThreads) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(row + 8 * c);
+    f16 cbest = (f16)(-__builtin_huge_valf());
+    int cidx = tid < V8 ? tid : -1;
+    f16x2 nsum = {(f16)0.f, (f16)0.f};
+    for (int c0 = tid; c0 < V8; c0 += kArgmaxThreads * kArgmaxLoads) {
+      u32x4 v[kArgmaxLoads];
 #pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const f16x2 h = as_h2(v[p]);
-        if (argmax_better((float)h.x, 8 * c + 2 * p, best, idx)) { best = (float)h.x; idx = 8 * c + 2 * p; }
-        if (argmax_better((float)h.y, 8 * c + 2 * p + 1, best, idx)) { best = (float)h.y; idx = 8 * c + 2 * p + 1; }
+      for (int u = 0; u < kArgmaxLoads; u++) {
+        const int c = c0 + u * kArgmaxThreads;
+        v[u] = c < V8 ? *reinterpret_cast<const u32x4*>(row + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < kArgmaxLoads; u++) {
+        const int c = c0 + u * kArgmaxThreads;
+        if (c < V8) {
+          const f16x2 x0 = as_h2(v[u][0]), x1 = as_h2(v[u][1]), x2 = as_h2(v[u][2]), x3 = as_h2(v[u][3]);
+          const f16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(x0, x1), __builtin_elementwise_max(x2, x3));
+          const f16 cm = m.x > m.y ? m.x : m.y;
+          nsum += (x0 + x1) + (x2 + x3);
+          if (cm > cbest) {
+            cbest = cm;
+            cidx = c;
+          }
+        }
       }
     }
-    for (int i = 8 * V8 + tid; i < V; i += kArgmaxThreads)
-      if (argmax_better((float)row[i], i, best, idx)) { best = (float)row[i]; idx = i; }
+    if (nsum.x != nsum.x || nsum.y != nsum.y) {
+      for (int c = tid; c < V8; c += kArgmaxThreads)
+        for (int i = 8 * c; i < 8 * c + 8; i++) scan(i);
+    } else if (cidx >= 0) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(row + 8 * cidx);
+      best = (float)cbest;
+      idx = 8 * cidx + 7;
+#pragma unroll
+      for (int e = 7; e >= 0; e--)  // the first logit equal to the chunk's max (-0 equals +0)
+        if ((float)as_h2(w[e >> 1])[e & 1] == best) idx = 8 * cidx + e;
+    }
+    for (int i = 8 * V8 + tid; i < V; i += kArgmaxThreads) scan(i);
   } else {
-    for (int i = tid; i < V; i += kArgmaxThreads)
-      if (argmax_better((float)row[i], i, best, idx)) { best = (float)row[i]; idx = i; }
+    for (int i = tid; i < V; i += kArgmaxThreads) scan(i);
   }
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(best, o, 64);
