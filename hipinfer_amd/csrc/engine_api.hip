@@ -272,6 +272,12 @@ int gemm(Engine* e, const void* A, int lda, const Wt& W, const f16* bias, void* 
   return hi_gemm(A, lda, W.w, bias, C, ldc, M, N, K, epi, e->st);
 }
 
+// X += A @ W^T, then Y = RMSNorm(X; nw): the residual GEMM and the norm that reads its result in
+// one call (the norm inside the split-K second pass when the GEMM splits K)
+int gemm_norm(Engine* e, const void* A, int lda, const Wt& W, f16* X, int M, int N, int K, const f16* nw, f16* Y) {
+  return hi_gemm_residual_rmsnorm(A, lda, W.w, W.s, X, M, N, K, nw, e->c.eps, Y, e->st);
+}
+
 // x[rows] += MoE(RMSNorm(x; n2)) (router + experts; api.cu:1694-1703)
 int moe_rows(Engine* e, const Layer& w, f16* x, f16* xn, int m) {
   const Cfg& c = e->c;
@@ -380,6 +386,7 @@ int decode_step(Engine* e, int B) {
     }
   }
   EN_TRY(hi_embed(e->tok, e->embed, V, H, e->x, H, B, s));
+  bool xn_ready = false;  // xn already holds RMSNorm(x) for the next consumer (from a down GEMM)
   for (int l = 0; l < c.layers; l++) {
     const Layer& w = e->L[l];
     f16* kc = e->kc + e->layer_cache * l;
@@ -392,13 +399,15 @@ int decode_step(Engine* e, int B) {
         EN_TRY(hi_gemv_qkv_rope(e->x, H, w.n1, c.eps, w.qkv.w, w.bqkv, e->qkv, e->qkv_dim, B, H, Hq, Hkv, D, e->rope,
                                 e->pos, kc, vc, e->max_seq, s));
     } else {
-      EN_TRY(hi_rmsnorm(e->x, w.n1, e->xn, B, H, c.eps, s));
+      if (!xn_ready) EN_TRY(hi_rmsnorm(e->x, w.n1, e->xn, B, H, c.eps, s));
       EN_TRY(gemm(e, e->xn, H, w.qkv, w.bqkv, e->qkv, e->qkv_dim, B, e->qkv_dim, H, 0));
       EN_TRY(hi_rope_cache(e->qkv, e->qkv_dim, B, Hq, Hkv, D, e->rope, e->pos, 0, 0, kc, vc, e->max_seq, s));
     }
+    xn_ready = false;
     EN_TRY(hi_decode_attn(e->qkv, e->qkv_dim, kc, vc, e->max_seq, e->pos, e->att, HD, B, Hq, Hkv, D, e->work, s));
     if (small) EN_TRY(gemv(e, e->att, HD, nullptr, w.o, e->x, H, B, H, HD, 1));
-    else EN_TRY(gemm(e, e->att, HD, w.o, nullptr, e->x, H, B, H, HD, 1));
+    else if (c.moe) EN_TRY(gemm(e, e->att, HD, w.o, nullptr, e->x, H, B, H, HD, 1));
+    else EN_TRY(gemm_norm(e, e->att, HD, w.o, e->x, B, H, HD, w.n2, e->xn));
     if (c.moe) {
       EN_TRY(moe_rows(e, w, e->x, e->xn, B));
       continue;
@@ -412,16 +421,17 @@ int decode_step(Engine* e, int B) {
       }
       if (sg & kDownGemm) EN_TRY(gemm(e, e->act, I, w.down, nullptr, e->x, H, B, H, I, 1));
       else EN_TRY(gemv(e, e->act, I, nullptr, w.down, e->x, H, B, H, I, 1));
-    } else {
-      EN_TRY(hi_rmsnorm(e->x, w.n2, e->xn, B, H, c.eps, s));
+    } else {  // xn = RMSNorm(x; n2) from the o GEMM's call
       EN_TRY(gemm(e, e->xn, H, w.gu, nullptr, e->act, I, B, 2 * I, H, 2));
-      EN_TRY(gemm(e, e->act, I, w.down, nullptr, e->x, H, B, H, I, 1));
+      const f16* nn = l + 1 < c.layers ? e->L[l + 1].n1 : e->final_norm;
+      EN_TRY(gemm_norm(e, e->act, I, w.down, e->x, B, H, I, nn, e->xn));
+      xn_ready = true;
     }
   }
   if (small && !(sg & kLmGemm)) {
     EN_TRY(gemv(e, e->x, H, e->final_norm, e->lm, e->logits, V, B, V, H, 0));
   } else {
-    EN_TRY(hi_rmsnorm(e->x, e->final_norm, e->xn, B, H, c.eps, s));
+    if (!xn_ready) EN_TRY(hi_rmsnorm(e->x, e->final_norm, e->xn, B, H, c.eps, s));
     EN_TRY(gemm(e, e->xn, H, e->lm, nullptr, e->logits, V, B, V, H, 0));
   }
   EN_TRY(hi_argmax(e->logits, B, V, e->tok, s));
@@ -504,26 +514,30 @@ int prefill(Engine* e, int slot, const int* tokens, int T, int p0, f16* all_logi
     const int pb = p0 + t0;
     EN_TRY(hipMemcpyAsync(e->ptok, tokens + t0, (size_t)n * 4, hipMemcpyHostToDevice, s));
     EN_TRY(hi_embed(e->ptok, e->embed, V, H, e->x, H, n, s));
+    bool xn_ready = false;  // xn already holds RMSNorm(x) for the next consumer (from a down GEMM)
     for (int l = 0; l < c.layers; l++) {
       const Layer& w = e->L[l];
       f16* kc = e->kc + e->layer_cache * l;
       f16* vc = e->vc + e->layer_cache * l;
-      EN_TRY(hi_rmsnorm(e->x, w.n1, e->xn, n, H, c.eps, s));
+      if (!xn_ready) EN_TRY(hi_rmsnorm(e->x, w.n1, e->xn, n, H, c.eps, s));
+      xn_ready = false;
       EN_TRY(gemm(e, e->xn, H, w.qkv, w.bqkv, e->qkv, e->qkv_dim, n, e->qkv_dim, H, 0));
       EN_TRY(hi_rope_cache(e->qkv, e->qkv_dim, n, Hq, Hkv, D, e->rope, nullptr, pb, slot, kc, vc, e->max_seq, s));
       const size_t so = (size_t)slot * Hkv * e->max_seq * D;
       EN_TRY(hi_flash_prefill(e->qkv, e->qkv_dim, kc + so, vc + so, e->max_seq, e->att, HD, n, pb, Hq, Hkv, D, s));
-      EN_TRY(gemm(e, e->att, HD, w.o, nullptr, e->x, H, n, H, HD, 1));
       if (c.moe) {
+        EN_TRY(gemm(e, e->att, HD, w.o, nullptr, e->x, H, n, H, HD, 1));
         EN_TRY(moe_rows(e, w, e->x, e->xn, n));
         continue;
       }
-      EN_TRY(hi_rmsnorm(e->x, w.n2, e->xn, n, H, c.eps, s));
+      EN_TRY(gemm_norm(e, e->att, HD, w.o, e->x, n, H, HD, w.n2, e->xn));
       EN_TRY(gemm(e, e->xn, H, w.gu, nullptr, e->act, I, n, 2 * I, H, 2));
-      EN_TRY(gemm(e, e->act, I, w.down, nullptr, e->x, H, n, H, I, 1));
+      const f16* nn = l + 1 < c.layers ? e->L[l + 1].n1 : e->final_norm;
+      EN_TRY(gemm_norm(e, e->act, I, w.down, e->x, n, H, I, nn, e->xn));
+      xn_ready = true;
     }
     if (all_logits) {
-      EN_TRY(hi_rmsnorm(e->x, e->final_norm, e->xn, n, H, c.eps, s));
+      if (!xn_ready) EN_TRY(hi_rmsnorm(e->x, e->final_norm, e->xn, n, H, c.eps, s));
       EN_TRY(gemm(e, e->xn, H, e->lm, nullptr, all_logits + (size_t)t0 * V, V, n, V, H, 0));
     }
   }

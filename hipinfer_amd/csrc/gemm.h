@@ -64,6 +64,11 @@ struct GemmArgs {
   const int* grp_tiles;
   int grp_n;
   int64_t grp_wstride;
+  // epilogue 1 with split-K only: the second pass also writes norm_y = RMSNorm(C) * norm_w (rows
+  // of N <= 8192 halves, C and norm_y contiguous: ldc == N); nullptr: the plain second pass
+  const f16* norm_w;
+  f16* norm_y;
+  float norm_eps;
 };
 
 constexpr int kGemmBK = 64;
@@ -646,6 +651,73 @@ inline size_t gemm_lds_bytes(int cfg, bool q8) {
   return (size_t)c.kg * c.st * (c.bm * c.bk * 2 + c.bn * (q8 ? c.bk : 2 * c.bk));
 }
 
+// Split-K second pass of a residual GEMM fused with the RMSNorm that reads its result: one block
+// per row sums the row's partials in split order and adds the residual exactly as
+// gemm_splitk_reduce<1> does, writes the row back, and normalises it as rmsnorm_kernel does (the
+// same chunk ownership and summation order), so both outputs are bit-identical to the two
+// kernels run in turn. Rows of N <= 8192 halves (N % 8 == 0), C and y contiguous.
+static __global__ void __launch_bounds__(256) gemm_splitk_reduce_rmsnorm(const float* __restrict__ ws, int splits, int M,
+                                                                         int N, f16* C, const f16* __restrict__ w,
+                                                                         f16* __restrict__ y, float eps) {
+  constexpr int RC = 4;  // 16-byte chunks per thread (rmsnorm_kernel's register-held rows)
+  __shared__ float red[4];
+  const int tid = threadIdx.x, n8 = N / 8, row = blockIdx.x;
+  const int64_t plane = (int64_t)M * N;
+  f16* xr = C + (int64_t)row * N;
+  const float* pr = ws + (int64_t)row * N;
+  u32x4 hv[RC], wv[RC];
+#pragma unroll
+  for (int j = 0; j < RC; j++) {
+    const int c = tid + j * 256;
+    hv[j] = wv[j] = u32x4{0u, 0u, 0u, 0u};
+    if (c < n8) {
+      wv[j] = *reinterpret_cast<const u32x4*>(w + 8 * c);
+      f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = t0;
+      for (int z = 0; z < splits; z++) {
+        t0 += *reinterpret_cast<const f32x4*>(pr + z * plane + 8 * c);
+        t1 += *reinterpret_cast<const f32x4*>(pr + z * plane + 8 * c + 4);
+      }
+      const f16x8 r = *reinterpret_cast<const f16x8*>(xr + 8 * c);
+      f16x8 h;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        h[e] = r[e] + (f16)t0[e];
+        h[4 + e] = r[4 + e] + (f16)t1[e];
+      }
+      hv[j] = __builtin_bit_cast(u32x4, h);
+      *reinterpret_cast<u32x4*>(xr + 8 * c) = hv[j];
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < RC; j++)
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const f16x2 h = as_h2(hv[j][p]);
+      ss = dot2(h, h, ss);
+    }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float rs = 1.0f / __builtin_sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)N + eps);
+  f16* yr = y + (int64_t)row * N;
+#pragma unroll
+  for (int j = 0; j < RC; j++) {
+    const int c = tid + j * 256;
+    if (c >= n8) continue;
+    u32x4 o;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const f16x2 xh = as_h2(hv[j][p]), wh = as_h2(wv[j][p]);
+      f16x2 t;
+      t.x = wh.x * (f16)((float)xh.x * rs);
+      t.y = wh.y * (f16)((float)xh.y * rs);
+      o[p] = as_u32(t);
+    }
+    *reinterpret_cast<u32x4*>(yr + 8 * c) = o;
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, int BK, int KG>
 int gemm_launch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
   const size_t lds = gemm_lds_bytes(cfg, Q8);
@@ -657,7 +729,11 @@ int gemm_launch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
   hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, EPI, Q8, false, BK, KG>), dim3(tiles, splits),
                      dim3(64 * WM * WN * KG), lds, s, g);
   HI_TRY(hipGetLastError());
-  if (splits > 1) {
+  if (splits > 1 && EPI == 1 && g.norm_y) {
+    hipLaunchKernelGGL(gemm_splitk_reduce_rmsnorm, dim3(g.M), dim3(256), 0, s, g.ws, splits, g.M, g.N, g.C, g.norm_w,
+                       g.norm_y, g.norm_eps);
+    HI_TRY(hipGetLastError());
+  } else if (splits > 1) {
     const int64_t quads = (int64_t)g.M * (EPI == 2 ? g.N / 2 : g.N) / 4;
     hipLaunchKernelGGL(gemm_splitk_reduce<EPI>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, g.ws, splits,
                        g.M, g.N, g.bias, g.C, g.ldc, g.vec_c);

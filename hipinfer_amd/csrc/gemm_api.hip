@@ -18,6 +18,7 @@
 #include <tuple>
 #include <vector>
 
+#include "../../include/hipinfer.h"
 #include "gemm.h"
 
 template <> int gemm_run<0>(const GemmArgs&, int, int, bool, hipStream_t);
@@ -113,7 +114,8 @@ int ensure_ws(size_t bytes, hipStream_t s, bool* ok) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s, float* fixed_ws = nullptr);
+int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s, float* fixed_ws = nullptr,
+                  int* used_splits = nullptr);
 
 // First-call autotuning per (M bucket, N, K, SwiGLU, int8) and device, as the reference's
 // gemm_choose (api.cu:465-552): every valid (tile, split) is timed on the real activations into a
@@ -233,7 +235,7 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
 // Launch with a chosen (tile, split): sets up the split-K workspace (or falls back to one split
 // when it would have to grow inside stream capture). With fixed_ws the partials go there instead,
 // and the caller has checked that they fit.
-int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s, float* fixed_ws) {
+int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s, float* fixed_ws, int* used_splits) {
   const HiDevice* d = hi_device();
   if (!d) return -2;
   GemmArgs g = g0;
@@ -264,6 +266,7 @@ int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s
   }
   g.kt_per_split = kps;
   g_last = ch;
+  if (used_splits) *used_splits = ch.splits;
   switch (epi) {
     case 0: return gemm_run<0>(g, ch.cfg, ch.splits, q8, s);
     case 1: return gemm_run<1>(g, ch.cfg, ch.splits, q8, s);
@@ -300,8 +303,11 @@ int gemm_args(const void* A, int lda, const void* W, const void* scales, const v
   return 0;
 }
 
+// norm_y non-null (epilogue 1, ldc == N): afterwards norm_y = RMSNorm(C) * norm_w, inside the
+// split-K second pass when the launch splits K and N <= 8192, else by hi_rmsnorm.
 int gemm_entry(const void* A, int lda, const void* W, const void* scales, const void* bias, void* C, int ldc, int M,
-               int N, int K, int epi, void* stream, const char* who) {
+               int N, int K, int epi, void* stream, const char* who, const void* norm_w = nullptr,
+               void* norm_y = nullptr, float eps = 0.f) {
   const HiDevice* d = hi_device();
   if (!d) return -2;
   GemmArgs g;
@@ -317,7 +323,16 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
     return r;
   }
   if (g_force_splits >= 1) ch.splits = g_force_splits;
-  return launch_choice(g, ch, epi, q8, s);
+  if (!norm_y) return launch_choice(g, ch, epi, q8, s);
+  const bool fuse = N <= 8192;
+  if (fuse) {  // set after the choice: the tuner times the plain second pass
+    g.norm_w = (const f16*)norm_w;
+    g.norm_y = (f16*)norm_y;
+    g.norm_eps = eps;
+  }
+  int used = 1;
+  if (int r = launch_choice(g, ch, epi, q8, s, nullptr, &used)) return r;
+  return fuse && used > 1 ? 0 : hi_rmsnorm(C, norm_w, norm_y, M, N, eps, stream);
 }
 
 }  // namespace
@@ -393,6 +408,20 @@ HI_EXPORT int hi_gemm_noalloc(const void* A, int lda, const void* W, const void*
     while (ch.splits > 1 && (size_t)ch.splits * per_split > kScratchBytes) ch.splits--;
   }
   return launch_choice(g, ch, epi, q8, (hipStream_t)stream, ws);
+}
+
+// X[M, N] += A[M, K] @ W[N, K]^T (epilogue 1, X contiguous), then Y = RMSNorm(X) * norm_w, as
+// hi_gemm / hi_gemm_w8 (scales non-null) followed by hi_rmsnorm, with the same results bit for bit.
+// When the launch splits K, the norm runs inside the split-K second pass (one kernel instead of
+// two, one read of X fewer). No counterpart in the reference, whose engine runs the two in turn.
+HI_EXPORT int hi_gemm_residual_rmsnorm(const void* A, int lda, const void* W, const void* scales, void* X, int M, int N,
+                                       int K, const void* norm_w, float eps, void* Y, void* stream) {
+  const char* who = "hi_gemm_residual_rmsnorm";
+  if (M < 0) HI_FAIL("%s: M %d < 0", who, M);
+  if (M == 0) return 0;
+  if (!X || !Y || !norm_w || !aligned(X, 16) || !aligned(Y, 16) || !aligned(norm_w, 16))
+    HI_FAIL("%s: X, Y and norm_w must be 16-byte aligned device pointers", who);
+  return gemm_entry(A, lda, W, scales, nullptr, X, N, M, N, K, 1, stream, who, norm_w, Y, eps);
 }
 
 // C (epi) A[M, K] @ W[N, K]^T (+ bias[N] for epi 0 when non-null), fp16 weights.

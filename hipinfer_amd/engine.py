@@ -101,13 +101,16 @@ class DecodeStep:
     def _ws(W):
         return (W[0], W[1]) if isinstance(W, tuple) else (W, None)
 
-    def _mlp_gemm(self, ly, x, xn, act, eps):
-        """x += SwiGLU(RMSNorm(x; n2) @ Wgu^T) @ Wdown^T on the GEMM (rows of x)."""
-        hi.rmsnorm(x, ly["n2"], eps, out=xn)
+    def _attn_mlp_gemm(self, ly, att, x, xn, act, eps, next_norm):
+        """x += o(att); x += SwiGLU(RMSNorm(x; n2) @ Wgu^T) @ Wdown^T on the GEMM (rows of x), each
+        residual GEMM with the RMSNorm that reads its result (n2 after o; next_norm, the next layer's
+        n1 or the final norm, after down) in one call. Leaves RMSNorm(x; next_norm) in xn."""
+        Wo, so = self._ws(ly["o"])
+        hi.gemm_rmsnorm(att, Wo, x, ly["n2"], eps, out=xn, scales=so)
         Wg, sg = self._ws(ly["gate_up"])
         hi.gemm(xn, Wg, out=act, epi=2, scales=sg)
         Wd, sd = self._ws(ly["down"])
-        hi.gemm(act, Wd, out=x, epi=1, scales=sd)
+        hi.gemm_rmsnorm(act, Wd, x, next_norm, eps, out=xn, scales=sd)
 
     def _tune_small_paths(self, eps):
         """Time gate/up, down and lm_head on the GEMV path and on the GEMM path (with the RMSNorm
@@ -162,10 +165,12 @@ class DecodeStep:
             self.small_gemm = 0 if torch.cuda.is_current_stream_capturing() else self._tune_small_paths(eps)
         sg = self.small_gemm
         hi.embed(self.tok, w["embed"], out=self.x)
-        for l, ly in enumerate(w["layers"]):
+        layers = w["layers"]
+        if self.gemm_path:  # later layers' norm (and the final one) come with the previous down GEMM
+            hi.rmsnorm(self.x, layers[0]["n1"], eps, out=self.xn)
+        for l, ly in enumerate(layers):
             Wq, sq = self._ws(ly["qkv"])
             if self.gemm_path:
-                hi.rmsnorm(self.x, ly["n1"], eps, out=self.xn)
                 hi.gemm(self.xn, Wq, out=self.qkv, bias=ly.get("bqkv"), scales=sq)
                 hi.rope_cache(self.qkv, Hq, Hkv, self.cs, self.kc[l], self.vc[l], pos=self.pos)
                 q = self.qkv[:, :Hq * D]
@@ -174,11 +179,11 @@ class DecodeStep:
                                  bias=ly.get("bqkv"), eps=eps, scales=sq)
                 q = self.q
             hi.decode_attn(q, self.kc[l], self.vc[l], self.pos, Hq, Hkv, out=self.att, work=self.work)
-            Wo, so = self._ws(ly["o"])
             if self.gemm_path:
-                hi.gemm(self.att, Wo, out=self.x, epi=1, scales=so)
-                self._mlp_gemm(ly, self.x, self.xn, self.act, eps)
+                nxt = layers[l + 1]["n1"] if l + 1 < len(layers) else w["nf"]
+                self._attn_mlp_gemm(ly, self.att, self.x, self.xn, self.act, eps, nxt)
             else:
+                Wo, so = self._ws(ly["o"])
                 hi.gemv(self.att, Wo, out=self.x, epi=1, scales=so)
                 Wg, s_g = self._ws(ly["gate_up"])
                 if sg & GU_GEMM:
@@ -193,7 +198,8 @@ class DecodeStep:
                     hi.gemv(self.act, Wd, out=self.x, epi=1, scales=sd)
         Wl, sl = self._ws(w["lm"])
         if self.gemm_path or sg & LM_GEMM:
-            hi.rmsnorm(self.x, w["nf"], eps, out=self.xn)
+            if not self.gemm_path:
+                hi.rmsnorm(self.x, w["nf"], eps, out=self.xn)
             hi.gemm(self.xn, Wl, out=self.logits, scales=sl)
         else:
             hi.gemv(self.x, Wl, out=self.logits, normw=w["nf"], eps=eps, scales=sl)
@@ -226,15 +232,15 @@ class DecodeStep:
             self.ptok[:n].copy_(toks[t0:t0 + n])
             x, xn, qkv, att, act = self.px[:n], self.pxn[:n], self.pqkv[:n], self.patt[:n], self.pact[:n]
             hi.embed(self.ptok[:n], w["embed"], out=x)
-            for l, ly in enumerate(w["layers"]):
-                hi.rmsnorm(x, ly["n1"], eps, out=xn)
+            layers = w["layers"]
+            hi.rmsnorm(x, layers[0]["n1"], eps, out=xn)  # later layers': the previous down GEMM's call
+            for l, ly in enumerate(layers):
                 Wq, sq = self._ws(ly["qkv"])
                 hi.gemm(xn, Wq, out=qkv, bias=ly.get("bqkv"), scales=sq)
                 hi.rope_cache(qkv, Hq, Hkv, self.cs, self.kc[l], self.vc[l], pos_base=pb, slot_base=slot)
                 hi.flash_prefill(qkv[:, :Hq * D], self.kc[l][slot], self.vc[l][slot], n, pb, Hq, Hkv, out=att)
-                Wo, so = self._ws(ly["o"])
-                hi.gemm(att, Wo, out=x, epi=1, scales=so)
-                self._mlp_gemm(ly, x, xn, act, eps)
+                nxt = layers[l + 1]["n1"] if l + 1 < len(layers) else w["nf"]
+                self._attn_mlp_gemm(ly, att, x, xn, act, eps, nxt)
         Wl, sl = self._ws(w["lm"])
         hi.gemv(x[n - 1:n], Wl, out=self.logits[slot:slot + 1], normw=w["nf"], eps=eps, scales=sl)
         hi.argmax(self.logits[slot:slot + 1], out=self.tok[slot:slot + 1])

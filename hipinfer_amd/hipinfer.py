@@ -58,6 +58,8 @@ int hi_gemm_force_splits(int splits);
 int hi_gemm_num_configs();
 int hi_gemm_config_desc(int cfg, str out, int n);
 int hi_gemm_last_choice(ptr cfg, ptr splits);
+int hi_gemm_residual_rmsnorm(ptr A, int lda, ptr W, ptr scales, ptr X, int M, int N, int K, ptr norm_w, float eps,
+                             ptr Y, ptr stream);
 int hi_gemm_noalloc(ptr A, int lda, ptr W, ptr scales, ptr bias, ptr C, int ldc, int M, int N, int K, int epi,
                     ptr stream);
 int hi_moe_router(ptr xn, int ldx, ptr Wr, int M, int E, int H, int k, int flags, ptr idx, ptr w, ptr stream);
@@ -237,6 +239,24 @@ def gemm(A, W, out=None, epi=0, bias=None, scales=None):
     rc = lib.hi_gemm_w8(*head, ptr(scales), *tail) if q8 else lib.hi_gemm(*head, *tail)
     check_rc(rc, "gemm")
     return out
+
+
+def gemm_rmsnorm(A, W, x, normw, eps=1e-5, out=None, scales=None):
+    """x += A @ W^T (the residual epilogue), then RMSNorm of the new x into out: the same bits as
+    gemm(A, W, out=x, epi=1) followed by rmsnorm(x, normw), with the norm inside the split-K second
+    pass when the GEMM splits K. x and out packed [M, N]."""
+    _need("gemm_rmsnorm", A, torch.float16, 2, rows=True)
+    _weight("gemm_rmsnorm", W, scales)
+    for t in (x, normw):
+        _need("gemm_rmsnorm", t, torch.float16)
+    y = torch.empty_like(x) if out is None else out
+    _need("gemm_rmsnorm", y, torch.float16)
+    if not (x.is_contiguous() and y.is_contiguous()):
+        raise ValueError("hipinfer_amd.gemm_rmsnorm: rows of x and out must be packed")
+    M, K = A.shape
+    check_rc(lib.hi_gemm_residual_rmsnorm(ptr(A), A.stride(0), ptr(W), ptr(scales), ptr(x), M, W.shape[0], K,
+                                          ptr(normw), eps, ptr(y), cur_stream()), "gemm_rmsnorm")
+    return y
 
 
 def gemm_noalloc(A, W, out, epi=0, bias=None, scales=None):

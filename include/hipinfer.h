@@ -81,6 +81,15 @@ int hi_gemm_last_choice(int* cfg, int* splits);
 int hi_gemm_noalloc(const void* A, int lda, const void* W, const void* scales, const void* bias, void* C, int ldc,
                     int M, int N, int K, int epi, void* stream);
 
+/* X[M, N] += A[M, K] @ W[N, K]^T (the residual epilogue 1, X contiguous: ldc == N), then
+ * Y[M, N] = RMSNorm(X) * norm_w (hi_rmsnorm's rule); scales NULL for fp16 W, else int8 W with fp16
+ * row scales. No counterpart in the reference: its engine runs the residual GEMM and the RMSNorm
+ * that reads it in turn (api.cu:1668-1690). This entry gives the same bits as hi_gemm(epi 1) then
+ * hi_rmsnorm, and when the GEMM splits K it runs the norm inside the split-K second pass (one
+ * kernel fewer, one read of X fewer). X, Y, norm_w 16-byte aligned. Returns 0, -1 or -2. */
+int hi_gemm_residual_rmsnorm(const void* A, int lda, const void* W, const void* scales, void* X, int M, int N, int K,
+                             const void* norm_w, float eps, void* Y, void* stream);
+
 /* ---- mixture of experts (fp16 experts, E <= 256, k <= 16)
  * Router + top-k of M normalised rows xn[M, H] under Wr[E, H]: idx[M, k] int, w[M, k] fp32, descending;
  * flags bit 0 = softmax over the k (else over all E), bit 1 = weights rounded to fp16.

@@ -473,3 +473,43 @@ def test_gemm_llama32_3b_layer(hi, O, M, q8):
         gemm_check(hi, O, f"C3 {name} {'int8' if q8 else 'fp16'} M={M}", A, W, r, epi=epi, scales=s, res=res, tol=tol)
         c, sp = last_choice(hi)
         assert 0 <= c < NUM_CFGS and sp >= 1, (name, c, sp)
+
+
+@pytest.mark.parametrize("q8", [False, True], ids=["fp16", "int8"])
+def test_gemm_residual_rmsnorm_bit_identical(hi, O, q8):
+    """hi_gemm_residual_rmsnorm gives the bits of hi_gemm (epilogue 1) followed by hi_rmsnorm, for
+    the new residual stream and its norm alike: on split-K launches (the norm inside the split-K
+    second pass), unsplit ones and the automatic choice, at a short M, and for rows wider than
+    the fused pass takes (N = 8704 > 8192: the separate norm). Sampled rows against the oracle."""
+    import torch
+    r = rng(520 + q8)
+    try:
+        for M, N, K in [(96, 4096, 1024), (300, 2048, 1536), (7, 1024, 512), (64, 8704, 512)]:
+            A, x0 = h16(r, M, K), h16(r, M, N)
+            W = h16(r, N, K, sd=0.02)
+            nw = (r.random(N) + 0.5).astype(np.float16)
+            s = None
+            if q8:
+                W, s = O.quantize_rows(W)
+            Ad, Wd, nd = cuda(A), cuda(W), cuda(nw)
+            sd = None if s is None else cuda(s)
+            for sp in (-1, 1, 2, 3):
+                hi.lib.hi_gemm_force_splits(sp)
+                xa = cuda(x0)
+                hi.gemm(Ad, Wd, out=xa, epi=1, scales=sd)
+                ya = hi.rmsnorm(xa, nd, 1e-5)
+                ran = last_choice(hi)
+                xb = cuda(x0)
+                yb = hi.gemm_rmsnorm(Ad, Wd, xb, nd, 1e-5, scales=sd)
+                assert last_choice(hi) == ran, (M, N, K, sp, ran, last_choice(hi))
+                if sp > 1:
+                    assert ran[1] > 1, f"split {sp} did not run at M={M} N={N} K={K}"
+                what = f"M={M} N={N} K={K} splits={sp} ran={ran}"
+                assert np.array_equal(bits(host(xa)), bits(host(xb))), f"residual stream differs: {what}"
+                assert np.array_equal(bits(host(ya)), bits(host(yb))), f"norm differs: {what}"
+            rows = sample_rows(M, r, 8)
+            xr = O.gemm(np.ascontiguousarray(A[rows]), W, out=np.ascontiguousarray(x0[rows]), epi=1, scales=s)
+            check(f"gemm_rmsnorm vs oracle M={M} N={N}", host(yb)[rows], O.rmsnorm(xr, nw), 4e-3, 4e-3)
+            torch.cuda.synchronize()
+    finally:
+        hi.lib.hi_gemm_force_splits(-1)
