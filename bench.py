@@ -673,6 +673,32 @@ def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
             "pct_hbm_peak": round(100 * 2 * nbytes / us / 1e3 / HBM_PEAK_GBS, 1)}
 
 
+def prefill_breakdown(csv_path):
+    """Per-kernel time of the last engine prefill in a rocprofv3 kernel trace (`--kernel-trace
+    --output-format csv`) of `bench.py --profile prefill`: the launches after the second-to-last
+    greedy argmax up to the last one (one whole prefill: embed, 32 layers, lm_head, argmax).
+    Prints a markdown table, longest total first."""
+    import csv
+    with open(csv_path) as f:
+        rows = sorted(((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
+                       for r in csv.DictReader(f)), key=lambda t: t[0])
+    ends = [i for i, r in enumerate(rows) if "argmax" in r[2]]
+    seg = rows[ends[-2] + 1:ends[-1] + 1]
+    span = (seg[-1][1] - seg[0][0]) / 1e3
+    agg = {}
+    for start, end, name in seg:
+        d = agg.setdefault(name.split("(")[0], [0, 0.0])
+        d[0] += 1
+        d[1] += (end - start) / 1e3
+    busy = sum(v[1] for v in agg.values())
+    print(f"prefill span (first launch start to last launch end): {span:.1f} us; kernels busy {busy:.1f} us; "
+          f"{len(seg)} launches")
+    print("| kernel | launches | avg us | total us | share of busy |")
+    print("|---|---|---|---|---|")
+    for name, (c, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        print(f"| `{name[:80]}` | {c} | {t / c:.2f} | {t:.1f} | {100 * t / busy:.1f} % |")
+
+
 def timeline(csv_path):
     """Per-kind durations and launch gaps of replayed decode tokens, from a rocprofv3 kernel trace
     (`--kernel-trace --output-format csv`) of `bench.py --profile token` / `token8`. A token is the
@@ -860,6 +886,9 @@ def main():
     if len(sys.argv) >= 3 and sys.argv[1] == "--gemm-counters":
         gemm_counters(sys.argv[2:])
         return
+    if len(sys.argv) == 3 and sys.argv[1] == "--prefill-breakdown":
+        prefill_breakdown(sys.argv[2])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -870,7 +899,10 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C4 / C5 sections")
     ap.add_argument("--no-step", action="store_true", help="skip the whole decode step (with attention) section")
     ap.add_argument("--no-engine", action="store_true", help="skip the engine prefill / batched decode section")
-    ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe", "c4"] +
+    ap.add_argument("--prefill-breakdown", metavar="CSV", default=None,
+                    help="(alone) print the per-kernel table of the last prefill in a kernel trace of "
+                         "--profile prefill")
+    ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe", "c4", "prefill"] +
                     [k + q for k in ("qkv", "o", "gate_up", "down", "lm_head") for q in ("", "8")], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
     args = ap.parse_args()
@@ -888,6 +920,20 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)}, {hi.lib.hi_device_cus()} CUs")
     if args.profile == "moe":
         log(json.dumps(moe_bench(torch, hi, args.steps, SEED + 12)))
+        return
+    if args.profile == "prefill":  # engine prefill of a 1024-token prompt, fp16: a tuning call, then 3
+        model = Model(torch, hi, q8_too=False)
+        from hipinfer_amd.engine import DecodeStep
+        g = torch.Generator(device="cuda")
+        g.manual_seed(SEED + 21)
+        embed = torch.empty(V, H, dtype=torch.float16, device="cuda").normal_(0.0, 1.0, generator=g)
+        cfg = dict(H=H, Hq=HQ, Hkv=HKV, D=D, I=I, V=V, L=L, eps=1e-5, theta=500000.0)
+        toks = torch.randint(0, V, (1024,), generator=torch.Generator().manual_seed(SEED + 22)).tolist()
+        ds = DecodeStep(cfg, engine_weights(model, embed, False), 1, 1024 + 16, max_prefill=1024)
+        for _ in range(4):
+            ds.prefill(0, toks)
+        torch.cuda.synchronize()
+        log("profile run done (prefill)")
         return
     if args.profile == "c4":  # the C4 GEMV set at 8 rows (speculative-verify width), fp16 then int8
         log(json.dumps(decode_config_bench(torch, hi, "C4 at 8 rows", C4_DIMS, [8], 28, args.steps, SEED + 11,
