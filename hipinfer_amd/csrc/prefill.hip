@@ -20,8 +20,9 @@
 //  * logits are scaled by log2(e) / sqrt(D) and the softmax runs in base 2 (the reference's
 //    log2-domain form, kernels.cuh:1236-1262); P is rounded to fp16 for P.V, the row sum l keeps
 //    fp32 p, as the reference does. exp2 is the hardware's v_exp_f32, whose results below 2^-126
-//    flush to zero: such p round to fp16 zero anyway and vanish against l >= 1 in fp32. O is
-//    rescaled only when some row's running max moved;
+//    flush to zero: such p round to fp16 zero anyway and vanish against l >= 1 in fp32. A row's
+//    reference max moves only when the row's max passes it by more than 2^8 (p <= 256), and O is
+//    rescaled only then;
 //  * O^T += V^T P^T: the P registers of a lane are already a B fragment of the next product once
 //    the key order inside each 16-key step is permuted identically for P and V^T (lane half fk
 //    takes keys 4 fk + 0..3 and 8 + 4 fk + 0..3), so P never goes through LDS. The V^T fragments
@@ -40,6 +41,7 @@ constexpr int kFpRG = 4;              // 32-row groups per block (2 waves each)
 constexpr int kFpBQ = 32 * kFpRG;     // query rows per block
 constexpr int kFpBKV = 64;            // keys per tile
 constexpr int kFpStages = 2;          // LDS stages of K/V tiles
+constexpr float kFpMaxLag = 8.f;      // log2 of how far a row's reference max may trail its max
 
 // XOR term of key r's 16-byte chunks in the K tile: the 16 keys (D = 128) or 8 key pairs (D = 64)
 // that one 128-bit fragment read serves per cycle land on distinct banks.
@@ -156,6 +158,10 @@ __global__ void __launch_bounds__(128 * RG)
   const int vsw = v_swz<D>(vr), vh = 4 * (lane & 1);           // swizzle term, half within the chunk
   const int kr = 32 * kh + fr;                                 // K row of this lane's fragments
   const int ksw = k_swz<D>(kr);
+  const int xaddr = (lane ^ 32) << 2;                          // lane l ^ 32, for ds_bpermute
+  auto xor32 = [&](float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(xaddr, __builtin_bit_cast(int, v)));
+  };
 
   float m_i = -__builtin_huge_valf(), l_i = 0.f;
   f32x16 o[DT];
@@ -184,41 +190,41 @@ __global__ void __launch_bounds__(128 * RG)
       const f16x8 kf = __builtin_bit_cast(f16x8, ks_[kr * CPR + ((2 * ks + fk) ^ ksw)]);
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s, 0, 0, 0);
     }
-    // ---- online softmax of row qi over these keys (base 2)
+    // ---- online softmax of row qi over these keys (base 2). The row's reference max m_i moves
+    //      only when the tile's scaled max exceeds it by more than 2^8, so p = exp2(c s - m_i) stays
+    //      at most 256 (exact range for fp16 P and fp32 sums) and O is rescaled only then; the
+    //      max of the raw logits is scaled once (c > 0 keeps the order) and c s - m_i is one fma
     float mx = -__builtin_huge_valf();
     if (full) {
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        s[e] *= scale_log2;
-        mx = fmaxf(mx, s[e]);
-      }
+      for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[e]);
     } else {
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const int kp = k0 + 8 * (e >> 2) + 4 * fk + (e & 3);
-        const float v = (kp <= qpos && kp < kv_end) ? s[e] * scale_log2 : -__builtin_huge_valf();
+        const float v = (kp <= qpos && kp < kv_end) ? s[e] : -__builtin_huge_valf();
         s[e] = v;
         mx = fmaxf(mx, v);
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_i, mx);
-    // m_new is -inf only for a row that has seen no key yet (a row past T, or one whose first
-    // key lies in the other half): then every p and alpha is taken as 0 and 1
-    const float m_use = m_new == -__builtin_huge_valf() ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
+    mx = fmaxf(mx, xor32(mx)) * scale_log2;
+    const bool move = mx > m_i + kFpMaxLag;  // m_i = -inf: moves to the first finite max
+    const float alpha = move ? __builtin_amdgcn_exp2f(m_i - mx) : 1.f;
+    if (move) m_i = mx;
+    // m_i is -inf only for a row that has seen no key yet (a row past T, or one whose first key
+    // lies in the other half): every logit is then -inf and every p 0
+    const float m_use = m_i == -__builtin_huge_valf() ? 0.f : m_i;
     float sum = 0.f;
     f16x8 pf[2];
 #pragma unroll
     for (int e = 0; e < 16; e++) {
-      const float p = __builtin_amdgcn_exp2f(s[e] - m_use);
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], scale_log2, -m_use));
       sum += p;
       pf[e >> 3][e & 7] = (f16)p;
     }
-    sum += __shfl_xor(sum, 32);
+    sum += xor32(sum);
     l_i = l_i * alpha + sum;
-    m_i = m_new;
-    if (__any(alpha != 1.f)) {
+    if (__any(move)) {
 #pragma unroll
       for (int dt = 0; dt < DT; dt++)
 #pragma unroll
