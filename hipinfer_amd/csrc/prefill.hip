@@ -5,18 +5,19 @@
 //
 // Flash prefill for gfx950 (D = 64 or 128):
 //  * block = 32 RG query rows of one query head and 2 RG waves: the waves of row group g (g and
-//    g + RG) share its 32 rows and split every 64-key tile, keys 0..31 and 32..63, each with its
+//    g + RG) share its 32 rows and split every 128-key tile, keys 0..63 and 64..127, each with its
 //    own online-softmax state; the pair merges (m, l, O) through LDS at the end. Two waves per
 //    SIMD let one wave's softmax run beside the other's matrix work. The wave's Q rows stay in
 //    registers as v_mfma_f32_32x32x16_f16 operands for the whole kernel;
-//  * 64-key K/V tiles of the head's cache rows go straight from global memory into LDS by buffer
+//  * 128-key K/V tiles of the head's cache rows go straight from global memory into LDS by buffer
 //    DMA (no register staging), two LDS stages: tile j + 1 streams in while tile j is computed,
 //    one barrier per tile. Both tiles keep the cache's row-major order with their 16-byte chunks
 //    XOR-swizzled by the key; the swizzle is applied to the DMA's per-lane source address, since
 //    a DMA instruction writes 64 consecutive 16-byte LDS slots;
-//  * S^T = K Q^T over the wave's 32 keys: with the K fragment as first operand each lane ends with
-//    16 keys of ONE query row (split between lanes l and l + 32), so the row max and sum of the
-//    online softmax are the lane's own values plus one exchange with lane l ^ 32;
+//  * S^T = K Q^T over the wave's 64 keys, in 32-key MFMA blocks: with the K fragment as first
+//    operand each lane ends with 16 keys per block of ONE query row (split between lanes l and
+//    l + 32), so the row max and sum of the online softmax are the lane's own values plus one
+//    exchange with lane l ^ 32;
 //  * logits are scaled by log2(e) / sqrt(D) and the softmax runs in base 2 (the reference's
 //    log2-domain form, kernels.cuh:1236-1262); P is rounded to fp16 for P.V, the row sum l keeps
 //    fp32 p, as the reference does. exp2 is the hardware's v_exp_f32, whose results below 2^-126
@@ -39,7 +40,8 @@ namespace {
 
 constexpr int kFpRG = 4;              // 32-row groups per block (2 waves each)
 constexpr int kFpBQ = 32 * kFpRG;     // query rows per block
-constexpr int kFpBKV = 64;            // keys per tile
+constexpr int kFpKPW = 64;            // keys per wave per tile (32-key MFMA blocks of the wave's half)
+constexpr int kFpBKV = 2 * kFpKPW;    // keys per tile
 constexpr int kFpStages = 2;          // LDS stages of K/V tiles
 constexpr float kFpMaxLag = 8.f;      // log2 of how far a row's reference max may trail its max
 
@@ -156,8 +158,9 @@ __global__ void __launch_bounds__(128 * RG)
   const int vr = 4 * fk + ((lane & 15) >> 2);                  // key within a 16-key step
   const int vc0 = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);   // logical chunk within a 32-d tile
   const int vsw = v_swz<D>(vr), vh = 4 * (lane & 1);           // swizzle term, half within the chunk
-  const int kr = 32 * kh + fr;                                 // K row of this lane's fragments
-  const int ksw = k_swz<D>(kr);
+  constexpr int KT = kFpKPW / 32;                              // 32-key blocks per wave per tile
+  const int kr = kFpKPW * kh + fr;                             // K row of this lane's first fragments
+  const int ksw = k_swz<D>(kr);                                // the same for every block (kr % 16)
   const int xaddr = (lane ^ 32) << 2;                          // lane l ^ 32, for ds_bpermute
   auto xor32 = [&](float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(xaddr, __builtin_bit_cast(int, v)));
@@ -175,20 +178,24 @@ __global__ void __launch_bounds__(128 * RG)
     wait_vmcnt<0>();  // this wave's share of tile j0 is in LDS
     __syncthreads();  // every share is, and every wave is done with the other stage
     if (j0 + kFpBKV < kv_end) issue(j0 + kFpBKV, st ^ 1);
-    const int k0 = j0 + 32 * kh;                    // this wave's first key
+    const int k0 = j0 + kFpKPW * kh;                // this wave's first key
     if (k0 > p0 + qw + 31 || k0 >= kv_end) continue;  // every key of the half is masked for every row
-    const bool full = k0 + 31 <= p0 + qw && k0 + 32 <= kv_end;  // no key of the half is masked
+    const bool full = k0 + kFpKPW - 1 <= p0 + qw && k0 + kFpKPW <= kv_end;  // no key of the half is masked
     const u32x4* ks_ = sm[st].k;
     const f16* vs_ = reinterpret_cast<const f16*>(sm[st].v);
 
-    // ---- S^T = K Q^T over the wave's 32 keys; lane (row fr, half fk) gets keys 8 g + 4 fk + e
-    f32x16 s;
+    // ---- S^T = K Q^T over the wave's keys, 32 per block kt; lane (row fr, half fk) gets keys
+    //      32 kt + 8 g + 4 fk + e
+    f32x16 s[KT];
 #pragma unroll
-    for (int e = 0; e < 16; e++) s[e] = 0.f;
+    for (int kt = 0; kt < KT; kt++) {
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ks++) {
-      const f16x8 kf = __builtin_bit_cast(f16x8, ks_[kr * CPR + ((2 * ks + fk) ^ ksw)]);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s, 0, 0, 0);
+      for (int e = 0; e < 16; e++) s[kt][e] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ks++) {
+        const f16x8 kf = __builtin_bit_cast(f16x8, ks_[(kr + 32 * kt) * CPR + ((2 * ks + fk) ^ ksw)]);
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[kt], 0, 0, 0);
+      }
     }
     // ---- online softmax of row qi over these keys (base 2). The row's reference max m_i moves
     //      only when the tile's scaled max exceeds it by more than 2^8, so p = exp2(c s - m_i) stays
@@ -197,15 +204,19 @@ __global__ void __launch_bounds__(128 * RG)
     float mx = -__builtin_huge_valf();
     if (full) {
 #pragma unroll
-      for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[e]);
+      for (int kt = 0; kt < KT; kt++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[kt][e]);
     } else {
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int kp = k0 + 8 * (e >> 2) + 4 * fk + (e & 3);
-        const float v = (kp <= qpos && kp < kv_end) ? s[e] : -__builtin_huge_valf();
-        s[e] = v;
-        mx = fmaxf(mx, v);
-      }
+      for (int kt = 0; kt < KT; kt++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int kp = k0 + 32 * kt + 8 * (e >> 2) + 4 * fk + (e & 3);
+          const float v = (kp <= qpos && kp < kv_end) ? s[kt][e] : -__builtin_huge_valf();
+          s[kt][e] = v;
+          mx = fmaxf(mx, v);
+        }
     }
     mx = fmaxf(mx, xor32(mx)) * scale_log2;
     const bool move = mx > m_i + kFpMaxLag;  // m_i = -inf: moves to the first finite max
@@ -215,13 +226,15 @@ __global__ void __launch_bounds__(128 * RG)
     // lies in the other half): every logit is then -inf and every p 0
     const float m_use = m_i == -__builtin_huge_valf() ? 0.f : m_i;
     float sum = 0.f;
-    f16x8 pf[2];
+    f16x8 pf[KT][2];
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], scale_log2, -m_use));
-      sum += p;
-      pf[e >> 3][e & 7] = (f16)p;
-    }
+    for (int kt = 0; kt < KT; kt++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][e], scale_log2, -m_use));
+        sum += p;
+        pf[kt][e >> 3][e & 7] = (f16)p;
+      }
     sum += xor32(sum);
     l_i = l_i * alpha + sum;
     if (__any(move)) {
@@ -230,18 +243,21 @@ __global__ void __launch_bounds__(128 * RG)
 #pragma unroll
         for (int e = 0; e < 16; e++) o[dt][e] *= alpha;
     }
-    // ---- O^T += V^T P^T; step ss: lane half fk holds keys 16 ss + 4 fk + 0..3 and
-    //      16 ss + 8 + 4 fk + 0..3 of the wave's half, in P's registers and in the V^T reads alike
+    // ---- O^T += V^T P^T; step ss of block kt: lane half fk holds keys 32 kt + 16 ss + 4 fk + 0..3
+    //      and 32 kt + 16 ss + 8 + 4 fk + 0..3 of the wave's keys, in P's registers and in the V^T
+    //      reads alike
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-      for (int ss = 0; ss < 2; ss++) {
-        const int key = 32 * kh + 16 * ss + vr;
-        const f16* pa = vs_ + key * D + 8 * ((4 * dt + vc0) ^ vsw) + vh;
-        const f16x4 fa = lds_read_tr16(pa), fb = lds_read_tr16(pa + 8 * D);  // key + 8: same swizzle term
-        const f16x8 vf = {fa[0], fa[1], fa[2], fa[3], fb[0], fb[1], fb[2], fb[3]};
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ss], o[dt], 0, 0, 0);
-      }
+      for (int kt = 0; kt < KT; kt++)
+#pragma unroll
+        for (int ss = 0; ss < 2; ss++) {
+          const int key = kFpKPW * kh + 32 * kt + 16 * ss + vr;
+          const f16* pa = vs_ + key * D + 8 * ((4 * dt + vc0) ^ vsw) + vh;
+          const f16x4 fa = lds_read_tr16(pa), fb = lds_read_tr16(pa + 8 * D);  // key + 8: same swizzle term
+          const f16x8 vf = {fa[0], fa[1], fa[2], fa[3], fb[0], fb[1], fb[2], fb[3]};
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kt][ss], o[dt], 0, 0, 0);
+        }
   }
 
   // ---- merge the two key halves of each row group: the second wave hands (m, l, O) over
