@@ -123,14 +123,17 @@ int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s
 // best kept. Skipped under stream capture
 // and with HIPINFER_GEMM_AUTOTUNE=0 (the model above decides then).
 std::mutex g_tune_mu;
-std::map<std::tuple<int, int, int, int, bool, bool>, Choice> g_tuned;
+std::map<std::tuple<int, int, int, int, bool, bool, bool>, Choice> g_tuned;
 
-int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out) {
+// norm: the call is a residual GEMM followed by the RMSNorm of its result (hi_gemm_residual_rmsnorm):
+// each candidate is timed with that norm as it would run, inside the split-K second pass or as a
+// separate kernel after an unsplit launch, and the choice is kept apart from plain GEMMs'.
+int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out, bool norm = false) {
   const HiDevice* d = hi_device();
   if (!d) return -2;
   int mb = 16;
   while (mb < g.M && mb < 4096) mb *= 2;
-  const auto key = std::make_tuple(d->id, mb, g.N, g.K, epi == 2, q8);
+  const auto key = std::make_tuple(d->id, mb, g.N, g.K, epi == 2, q8, norm);
   {
     std::lock_guard<std::mutex> lk(g_tune_mu);
     auto it = g_tuned.find(key);
@@ -149,14 +152,26 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
 
   const int n_out = epi == 2 ? g.N / 2 : g.N;
   f16* scratch = nullptr;
-  HI_TRY(hipMalloc(&scratch, (size_t)g.M * n_out * sizeof(f16)));
-  HI_TRY(hipMemsetAsync(scratch, 0, (size_t)g.M * n_out * sizeof(f16), s));
+  HI_TRY(hipMalloc(&scratch, (size_t)g.M * n_out * sizeof(f16) * (norm ? 2 : 1) + (norm ? (size_t)g.N * sizeof(f16) : 0)));
+  HI_TRY(hipMemsetAsync(scratch, 0, (size_t)g.M * n_out * sizeof(f16) * (norm ? 2 : 1) + (norm ? (size_t)g.N * sizeof(f16) : 0), s));
   hipEvent_t e0, e1;
   HI_TRY(hipEventCreate(&e0));
   HI_TRY(hipEventCreate(&e1));
   GemmArgs t = g;
   t.C = scratch;
   t.ldc = n_out;
+  f16* norm_y = scratch + (size_t)g.M * n_out;  // norm: its output, then its (zero) weights
+  const f16* norm_w = norm_y + (size_t)g.M * n_out;
+  if (norm) {
+    t.norm_w = norm_w;
+    t.norm_y = norm_y;
+    t.norm_eps = 1e-5f;
+  }
+  auto launch = [&](Choice c) -> int {
+    int used = 1;
+    if (int rc = launch_choice(t, c, epi, q8, s, nullptr, &used)) return rc;
+    return norm && used == 1 ? hi_rmsnorm(t.C, norm_w, norm_y, g.M, g.N, 1e-5f, s) : 0;
+  };
   // Candidates are timed on rotating scratch weight buffers (at least ~640 MB in all, so neither
   // the L2s nor the 256 MB MALL hold them): a prefill streams each layer's weights once, and
   // timing on the same, cache-resident weights would favour tiles that re-read more. The scratch
@@ -172,11 +187,11 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
   }
   auto time_it = [&](Choice c, int reps, float* us) -> int {
     t.W = wrot ? wrot : g.W;
-    if (int rc = launch_choice(t, c, epi, q8, s)) return rc;
+    if (int rc = launch(c)) return rc;
     HI_TRY(hipEventRecord(e0, s));
     for (int r = 0; r < reps; r++) {
       if (wrot) t.W = wrot + (size_t)((r + 1) % nrot) * wstride;
-      if (int rc = launch_choice(t, c, epi, q8, s)) return rc;
+      if (int rc = launch(c)) return rc;
     }
     HI_TRY(hipEventRecord(e1, s));
     HI_TRY(hipEventSynchronize(e1));
@@ -199,8 +214,8 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
       rc = time_it({c, sp}, std::max(nrot, 4), &us);
       if (!rc) timed.push_back({us, {c, sp}});
       if (!rc && verbose >= 2)
-        fprintf(stderr, "hipinfer_amd gemm autotune M=%d N=%d K=%d epi=%d%s   cfg %d (%dx%d) split %d: %.1f us\n", g.M,
-                g.N, g.K, epi, q8 ? " int8" : "", c, bm, kGemmCfgs[c].bn, sp, us);
+        fprintf(stderr, "hipinfer_amd gemm autotune M=%d N=%d K=%d epi=%d%s%s   cfg %d (%dx%d) split %d: %.1f us\n",
+                g.M, g.N, g.K, epi, q8 ? " int8" : "", norm ? " +norm" : "", c, bm, kGemmCfgs[c].bn, sp, us);
     }
   }
   if (!rc && !timed.empty()) {
@@ -217,8 +232,8 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out)
       }
     }
     if (verbose && !rc)
-      fprintf(stderr, "hipinfer_amd gemm autotune M=%d N=%d K=%d epi=%d%s -> cfg %d split %d: %.1f us, %.1f TFLOP/s\n",
-              g.M, g.N, g.K, epi, q8 ? " int8" : "", out->cfg, out->splits, best,
+      fprintf(stderr, "hipinfer_amd gemm autotune M=%d N=%d K=%d epi=%d%s%s -> cfg %d split %d: %.1f us, %.1f TFLOP/s\n",
+              g.M, g.N, g.K, epi, q8 ? " int8" : "", norm ? " +norm" : "", out->cfg, out->splits, best,
               2.0 * g.M * g.N * g.K / (best * 1e-6) / 1e12);
   }
   (void)hipEventDestroy(e0);
@@ -319,7 +334,7 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
   if (g_force_cfg >= 0 && g_force_cfg < kGemmNumCfgs && gemm_cfg_fits(g_force_cfg, q8, K)) {  // else: automatic
     ch = gemm_pick(M, N, K, q8, d->cus);
     ch.cfg = g_force_cfg;
-  } else if (int r = gemm_choose(g, epi, q8, s, &ch)) {
+  } else if (int r = gemm_choose(g, epi, q8, s, &ch, norm_y != nullptr && N <= 8192)) {
     return r;
   }
   if (g_force_splits >= 1) ch.splits = g_force_splits;
@@ -393,7 +408,7 @@ HI_EXPORT int hi_gemm_noalloc(const void* A, int lda, const void* W, const void*
     int mb = 16;
     while (mb < M && mb < 4096) mb *= 2;
     std::lock_guard<std::mutex> lk(g_tune_mu);
-    auto it = g_tuned.find(std::make_tuple(d->id, mb, N, K, epi == 2, q8));
+    auto it = g_tuned.find(std::make_tuple(d->id, mb, N, K, epi == 2, q8, false));
     if (it != g_tuned.end()) ch = it->second;
   }
   const size_t per_split = (size_t)M * N * sizeof(float);

@@ -494,13 +494,18 @@ def test_gemm_residual_rmsnorm_bit_identical(hi, O, q8):
             Ad, Wd, nd = cuda(A), cuda(W), cuda(nw)
             sd = None if s is None else cuda(s)
             for sp in (-1, 1, 2, 3):
+                # the fused call first (automatic: its own tuning, which times the norm too), then
+                # the two calls forced onto the tile and split count it ran
+                hi.lib.hi_gemm_force_config(-1)
                 hi.lib.hi_gemm_force_splits(sp)
+                xb = cuda(x0)
+                yb = hi.gemm_rmsnorm(Ad, Wd, xb, nd, 1e-5, scales=sd)
+                ran = last_choice(hi)
+                hi.lib.hi_gemm_force_config(ran[0])
+                hi.lib.hi_gemm_force_splits(ran[1])
                 xa = cuda(x0)
                 hi.gemm(Ad, Wd, out=xa, epi=1, scales=sd)
                 ya = hi.rmsnorm(xa, nd, 1e-5)
-                ran = last_choice(hi)
-                xb = cuda(x0)
-                yb = hi.gemm_rmsnorm(Ad, Wd, xb, nd, 1e-5, scales=sd)
                 assert last_choice(hi) == ran, (M, N, K, sp, ran, last_choice(hi))
                 if sp > 1:
                     assert ran[1] > 1, f"split {sp} did not run at M={M} N={N} K={K}"
@@ -512,4 +517,5 @@ def test_gemm_residual_rmsnorm_bit_identical(hi, O, q8):
             check(f"gemm_rmsnorm vs oracle M={M} N={N}", host(yb)[rows], O.rmsnorm(xr, nw), 4e-3, 4e-3)
             torch.cuda.synchronize()
     finally:
+        hi.lib.hi_gemm_force_config(-1)
         hi.lib.hi_gemm_force_splits(-1)
