@@ -652,15 +652,21 @@ inline size_t gemm_lds_bytes(int cfg, bool q8) {
 }
 
 // Split-K second pass of a residual GEMM fused with the RMSNorm that reads its result: one block
-// per row sums the row's partials in split order and adds the residual exactly as
+// of kNormThreads per row sums the row's partials in split order and adds the residual exactly as
 // gemm_splitk_reduce<1> does, writes the row back, and normalises it as rmsnorm_kernel does (the
-// same chunk ownership and summation order), so both outputs are bit-identical to the two
-// kernels run in turn. Rows of N <= 8192 halves (N % 8 == 0), C and y contiguous.
-static __global__ void __launch_bounds__(256) gemm_splitk_reduce_rmsnorm(const float* __restrict__ ws, int splits, int M,
-                                                                         int N, f16* C, const f16* __restrict__ w,
-                                                                         f16* __restrict__ y, float eps) {
-  constexpr int RC = 4;  // 16-byte chunks per thread (rmsnorm_kernel's register-held rows)
-  __shared__ float red[4];
+// same chunk ownership, summation order and norm_finish), so both outputs are bit-identical to
+// the two kernels run in turn. With the split count ZS fixed at compile time (2..8) a thread issues
+// all its loads of a chunk's partials before it adds them: with one row per block the pass is
+// otherwise one memory round trip per split (ZS = 0: any count, one split at a time). RC chunks
+// per thread: 1 for rows of up to 4096 halves (rmsnorm_kernel's second chunk then only adds exact
+// zeros), else kNormChunks. Rows of N <= 8192 halves (N % 8 == 0), C and y contiguous.
+template <int RC, int ZS>
+__global__ void __launch_bounds__(kNormThreads) gemm_splitk_reduce_rmsnorm(const float* __restrict__ ws, int splits,
+                                                                           int M, int N, f16* C,
+                                                                           const f16* __restrict__ w,
+                                                                           f16* __restrict__ y, float eps) {
+  static_assert(RC >= 1 && RC <= kNormChunks, "chunks per thread");
+  __shared__ float red[kNormThreads / 64];
   const int tid = threadIdx.x, n8 = N / 8, row = blockIdx.x;
   const int64_t plane = (int64_t)M * N;
   f16* xr = C + (int64_t)row * N;
@@ -668,16 +674,30 @@ static __global__ void __launch_bounds__(256) gemm_splitk_reduce_rmsnorm(const f
   u32x4 hv[RC], wv[RC];
 #pragma unroll
   for (int j = 0; j < RC; j++) {
-    const int c = tid + j * 256;
+    const int c = tid + j * kNormThreads;
     hv[j] = wv[j] = u32x4{0u, 0u, 0u, 0u};
     if (c < n8) {
       wv[j] = *reinterpret_cast<const u32x4*>(w + 8 * c);
-      f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = t0;
-      for (int z = 0; z < splits; z++) {
-        t0 += *reinterpret_cast<const f32x4*>(pr + z * plane + 8 * c);
-        t1 += *reinterpret_cast<const f32x4*>(pr + z * plane + 8 * c + 4);
-      }
       const f16x8 r = *reinterpret_cast<const f16x8*>(xr + 8 * c);
+      f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = t0;
+      if constexpr (ZS > 0) {
+        f32x4 a[ZS], b[ZS];
+#pragma unroll
+        for (int z = 0; z < ZS; z++) {
+          a[z] = *reinterpret_cast<const f32x4*>(pr + z * plane + 8 * c);
+          b[z] = *reinterpret_cast<const f32x4*>(pr + z * plane + 8 * c + 4);
+        }
+#pragma unroll
+        for (int z = 0; z < ZS; z++) {
+          t0 += a[z];
+          t1 += b[z];
+        }
+      } else {
+        for (int z = 0; z < splits; z++) {
+          t0 += *reinterpret_cast<const f32x4*>(pr + z * plane + 8 * c);
+          t1 += *reinterpret_cast<const f32x4*>(pr + z * plane + 8 * c + 4);
+        }
+      }
       f16x8 h;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -696,14 +716,11 @@ static __global__ void __launch_bounds__(256) gemm_splitk_reduce_rmsnorm(const f
       const f16x2 h = as_h2(hv[j][p]);
       ss = dot2(h, h, ss);
     }
-  ss = wave_sum(ss);
-  if ((tid & 63) == 0) red[tid >> 6] = ss;
-  __syncthreads();
-  const float rs = 1.0f / __builtin_sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)N + eps);
+  const float rs = norm_finish(ss, red, N, eps);
   f16* yr = y + (int64_t)row * N;
 #pragma unroll
   for (int j = 0; j < RC; j++) {
-    const int c = tid + j * 256;
+    const int c = tid + j * kNormThreads;
     if (c >= n8) continue;
     u32x4 o;
 #pragma unroll
@@ -718,6 +735,23 @@ static __global__ void __launch_bounds__(256) gemm_splitk_reduce_rmsnorm(const f
   }
 }
 
+typedef void (*SplitkRmsnormFn)(const float*, int, int, int, f16*, const f16*, f16*, float);
+template <int RC>
+inline SplitkRmsnormFn splitk_rmsnorm_for(int splits) {
+  switch (splits) {
+    case 2: return gemm_splitk_reduce_rmsnorm<RC, 2>;
+    case 3: return gemm_splitk_reduce_rmsnorm<RC, 3>;
+    case 4: return gemm_splitk_reduce_rmsnorm<RC, 4>;
+    case 5: return gemm_splitk_reduce_rmsnorm<RC, 5>;
+    case 6: return gemm_splitk_reduce_rmsnorm<RC, 6>;
+    case 8: return gemm_splitk_reduce_rmsnorm<RC, 8>;
+    default: return gemm_splitk_reduce_rmsnorm<RC, 0>;
+  }
+}
+inline SplitkRmsnormFn splitk_rmsnorm_kernel(bool one_chunk, int splits) {
+  return one_chunk ? splitk_rmsnorm_for<1>(splits) : splitk_rmsnorm_for<kNormChunks>(splits);
+}
+
 template <int BM, int BN, int WM, int WN, int S, int EPI, bool Q8, int BK, int KG>
 int gemm_launch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
   const size_t lds = gemm_lds_bytes(cfg, Q8);
@@ -730,8 +764,8 @@ int gemm_launch(const GemmArgs& g, int cfg, int splits, hipStream_t s) {
                      dim3(64 * WM * WN * KG), lds, s, g);
   HI_TRY(hipGetLastError());
   if (splits > 1 && EPI == 1 && g.norm_y) {
-    hipLaunchKernelGGL(gemm_splitk_reduce_rmsnorm, dim3(g.M), dim3(256), 0, s, g.ws, splits, g.M, g.N, g.C, g.norm_w,
-                       g.norm_y, g.norm_eps);
+    hipLaunchKernelGGL(splitk_rmsnorm_kernel(g.N <= 8 * kNormThreads, splits), dim3(g.M), dim3(kNormThreads), 0, s, g.ws,
+                       splits, g.M, g.N, g.C, g.norm_w, g.norm_y, g.norm_eps);
     HI_TRY(hipGetLastError());
   } else if (splits > 1) {
     const int64_t quads = (int64_t)g.M * (EPI == 2 ? g.N / 2 : g.N) / 4;

@@ -86,6 +86,22 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
+// RMSNorm rows (rmsnorm_kernel, and the split-K second pass that normalises its result): one block
+// of kNormThreads per row; thread t holds chunks t + kNormThreads j (j < kNormChunks: rows of up
+// to 8192 halves) and sums their squares chunk by chunk. Both kernels finish with norm_finish, so
+// they round alike.
+constexpr int kNormThreads = 512;
+constexpr int kNormChunks = 2;
+// 1 / sqrt(mean(x^2) + eps) of the block's row from each thread's partial sum of squares: wave
+// sums, then the 8 wave partials pairwise. red: 8 floats of LDS.
+__device__ __forceinline__ float norm_finish(float ss, float* red, int H, float eps) {
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float t = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+  return 1.0f / __builtin_sqrtf(t / (float)H + eps);
+}
+
 // DPP row_ror:N (rotate right: data moves to higher lanes) into the lanes of the banks (groups of 4
 // lanes of a 16-lane row) in BANKS; the other lanes return old. Lane l reads lane
 // (l & ~15) | ((l - N) & 15).

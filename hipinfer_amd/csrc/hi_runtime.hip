@@ -197,24 +197,24 @@ HI_EXPORT int hi_dequantize_rows(const void* q, const void* s, long long N, int 
 }
 
 // ------------------------------------------------------------------ standalone RMSNorm
-// y = w * fp16(x * (1 / sqrt(mean x^2 + eps))), one block per row, rows contiguous.
-// One block per row. Rows of up to 8192 halves stay in registers between the sum of squares and
+// y = w * fp16(x * (1 / sqrt(mean x^2 + eps))), one block of kNormThreads per row, rows contiguous.
+// Rows of up to kNormChunks * kNormThreads chunks stay in registers between the sum of squares and
 // the scaling (one read of the row), and the norm weight is requested before the reduction; the
 // sums run in the same chunk order either way.
-__global__ void __launch_bounds__(256) rmsnorm_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
-                                                     f16* __restrict__ y, int H, float eps) {
-  constexpr int RC = 4;  // 16-byte chunks per thread held in registers
-  __shared__ float red[4];
+__global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
+                                                              f16* __restrict__ y, int H, float eps) {
+  constexpr int RC = kNormChunks;
+  __shared__ float red[kNormThreads / 64];
   const int tid = threadIdx.x, n8 = H / 8;
   const f16* xr = x + (int64_t)blockIdx.x * H;
   f16* yr = y + (int64_t)blockIdx.x * H;
-  const bool held = n8 <= RC * 256;
+  const bool held = n8 <= RC * kNormThreads;
   u32x4 xv[RC], wv[RC];
   float ss = 0.f;
   if (held) {
 #pragma unroll
     for (int j = 0; j < RC; j++) {
-      const int c = tid + j * 256;
+      const int c = tid + j * kNormThreads;
       xv[j] = c < n8 ? *reinterpret_cast<const u32x4*>(xr + 8 * c) : u32x4{0u, 0u, 0u, 0u};
       wv[j] = c < n8 ? *reinterpret_cast<const u32x4*>(w + 8 * c) : u32x4{0u, 0u, 0u, 0u};
     }
@@ -226,7 +226,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const f16* __restrict__ x,
         ss = dot2(h, h, ss);
       }
   } else {
-    for (int i = tid; i < n8; i += 256) {
+    for (int i = tid; i < n8; i += kNormThreads) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(xr + 8 * i);
 #pragma unroll
       for (int p = 0; p < 4; p++) {
@@ -235,10 +235,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const f16* __restrict__ x,
       }
     }
   }
-  ss = wave_sum(ss);
-  if ((tid & 63) == 0) red[tid >> 6] = ss;
-  __syncthreads();
-  const float r = 1.0f / __builtin_sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)H + eps);
+  const float r = norm_finish(ss, red, H, eps);
   auto scale = [&](u32x4 xc, u32x4 wc) {
     u32x4 o;
 #pragma unroll
@@ -254,11 +251,11 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const f16* __restrict__ x,
   if (held) {
 #pragma unroll
     for (int j = 0; j < RC; j++) {
-      const int c = tid + j * 256;
+      const int c = tid + j * kNormThreads;
       if (c < n8) *reinterpret_cast<u32x4*>(yr + 8 * c) = scale(xv[j], wv[j]);
     }
   } else {
-    for (int i = tid; i < n8; i += 256)
+    for (int i = tid; i < n8; i += kNormThreads)
       *reinterpret_cast<u32x4*>(yr + 8 * i) =
           scale(*reinterpret_cast<const u32x4*>(xr + 8 * i), *reinterpret_cast<const u32x4*>(w + 8 * i));
   }
@@ -269,8 +266,8 @@ HI_EXPORT int hi_rmsnorm(const void* x, const void* w, void* y, int M, int H, fl
   if (M == 0) return 0;
   if (!x || !w || !y || ((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)y & 15))
     HI_FAIL("hi_rmsnorm: x, w, y must be 16-byte aligned device pointers");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, (const f16*)x, (const f16*)w, (f16*)y, H,
-                     eps);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(kNormThreads), 0, (hipStream_t)stream, (const f16*)x, (const f16*)w,
+                     (f16*)y, H, eps);
   HI_TRY(hipGetLastError());
   return 0;
 }
