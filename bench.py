@@ -902,7 +902,7 @@ def main():
     ap.add_argument("--prefill-breakdown", metavar="CSV", default=None,
                     help="(alone) print the per-kernel table of the last prefill in a kernel trace of "
                          "--profile prefill")
-    ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe", "c4", "prefill"] +
+    ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe", "c4", "prefill", "flash"] +
                     [k + q for k in ("qkv", "o", "gate_up", "down", "lm_head") for q in ("", "8")], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
     args = ap.parse_args()
@@ -920,6 +920,19 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)}, {hi.lib.hi_device_cus()} CUs")
     if args.profile == "moe":
         log(json.dumps(moe_bench(torch, hi, args.steps, SEED + 12)))
+        return
+    if args.profile == "flash":  # flash prefill alone, Llama-3.1-8B heads, T = 1024 / 2048 / 4096, 10 launches each
+        g = torch.Generator(device="cuda")
+        g.manual_seed(SEED + 23)
+        for T in (1024, 2048, 4096):
+            kc = torch.empty(HKV, T, D, dtype=torch.float16, device="cuda").normal_(generator=g)
+            vc = torch.empty(HKV, T, D, dtype=torch.float16, device="cuda").normal_(generator=g)
+            qq = torch.empty(T, HQ * D, dtype=torch.float16, device="cuda").normal_(generator=g)
+            oo = torch.empty_like(qq)
+            for _ in range(10):
+                hi.flash_prefill(qq, kc, vc, T, 0, HQ, HKV, out=oo)
+            torch.cuda.synchronize()
+        log("profile run done (flash)")
         return
     if args.profile == "prefill":  # engine prefill of a 1024-token prompt, fp16: a tuning call, then 3
         model = Model(torch, hi, q8_too=False)
