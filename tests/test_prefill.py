@@ -96,6 +96,26 @@ def test_flash_prefill_fused_qkv_rows_and_lse(hi, O):
     check("flash prefill lse (log2 domain)", host(lse), ref_lse, 1e-4, 1e-5)
 
 
+@pytest.mark.parametrize("grow", [True, False], ids=["rising", "falling"])
+def test_flash_prefill_moving_max(hi, O, grow):
+    """Logits that rise (or fall) steeply along the keys: every key share of every tile moves each
+    row's running max by far more than the kernel's rescale lag (2^8), so the O rescale and the
+    merge of shares with very different maxima run on every tile (with random data a row's max
+    settles in its first tiles). Output and lse against the oracle."""
+    r = rng(1250 + grow)
+    D, Hq, Hkv, S, T, p0 = 128, 16, 8, 1024, 600, 40
+    u = np.sign(r.standard_normal(D))  # a fixed direction; q and k lean on it
+    pos = np.arange(S, dtype=np.float64)[:, None]
+    ramp = 0.03 * (pos if grow else (S - pos))
+    kc = (r.standard_normal((Hkv, S, D)) * 0.3 + ramp * u).astype(np.float16)
+    vc = r.standard_normal((Hkv, S, D)).astype(np.float16)
+    q = (np.tile(u, (T, Hq)) + r.standard_normal((T, Hq * D)) * 0.3).astype(np.float16)
+    out, lse = hi.flash_prefill_lse(cuda(q), cuda(kc), cuda(vc), T, p0, Hq, Hkv)
+    ref, ref_lse = O.flash_prefill(q, kc, vc, T, p0, Hq, Hkv, lse=True)
+    check(f"flash prefill, {'rising' if grow else 'falling'} logits", host(out), ref, 2e-3, 1e-2)
+    check(f"flash prefill lse, {'rising' if grow else 'falling'} logits", host(lse), ref_lse, 1e-4, 1e-5)
+
+
 def test_flash_prefill_rejects_bad_arguments(hi):
     import torch
     q = torch.zeros(4, 3 * 96, dtype=torch.float16, device="cuda")
