@@ -458,6 +458,9 @@ static int decode_attn_run(const void* q, int ldq, const void* kc, const void* v
   if (B < 0 || Hkv < 1 || Hq < Hkv || Hq % Hkv || Hq / Hkv > 8 || max_seq < 1)
     HI_FAIL("%s: B %d, Hq %d, Hkv %d (Hq / Hkv in 1..8), max_seq %d", who, B, Hq, Hkv, max_seq);
   if (B == 0) return 0;
+  if ((int64_t)max_seq * D * 2 > INT32_MAX)  // a head's cache rows are addressed by 32-bit byte offsets
+    HI_FAIL("%s: max_seq %d too long for 32-bit cache offsets (at most %d at D=%d)", who, max_seq,
+            (int)(INT32_MAX / (2 * D)), D);
   if (B * Hkv > kDecodeCounters) HI_FAIL("%s: B*Hkv %d > %d", who, B * Hkv, kDecodeCounters);
   if (!q || !kc || !vc || !pos || !out || !work) HI_FAIL("%s: null pointer", who);
   if (((uintptr_t)q & 15) || ldq % 8 || ((uintptr_t)kc & 15) || ((uintptr_t)vc & 15) || ((uintptr_t)work & 3) ||

@@ -359,6 +359,9 @@ int flash_prefill(const void* q, int ldq, const void* kc, const void* vc, int ma
   if (T < 0 || p0 < 0 || Hkv < 1 || Hq < Hkv || Hq % Hkv || max_seq < 1 || (int64_t)p0 + T > max_seq)
     HI_FAIL("%s: bad shape T=%d p0=%d Hq=%d Hkv=%d max_seq=%d", who, T, p0, Hq, Hkv, max_seq);
   if (T == 0) return 0;
+  if ((int64_t)max_seq * D * 2 > INT32_MAX)  // a head's cache rows are addressed by 32-bit byte offsets
+    HI_FAIL("%s: max_seq %d too long for 32-bit cache offsets (at most %d at D=%d)", who, max_seq,
+            (int)(INT32_MAX / (2 * D)), D);
   if (!q || !kc || !vc || !out) HI_FAIL("%s: null tensor pointer", who);
   if (!aligned(q, 16) || ldq % 8 || ldq < Hq * D) HI_FAIL("%s: q must be 16-byte aligned, ldq %% 8 == 0, ldq >= Hq*D", who);
   if (!aligned(kc, 16) || !aligned(vc, 16)) HI_FAIL("%s: kc / vc must be 16-byte aligned", who);

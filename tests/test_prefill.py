@@ -126,3 +126,8 @@ def test_flash_prefill_rejects_bad_arguments(hi):
     kc = torch.zeros(1, 64, 64, dtype=torch.float16, device="cuda")
     with pytest.raises(ValueError):
         hi.flash_prefill(q, kc, kc, 4, 61, 2, 1)  # p0 + T past max_seq
+    # a cache slot whose head rows pass 2 GiB (32-bit offsets) is refused before anything runs
+    out = torch.empty_like(q)
+    rc = hi.lib.hi_flash_prefill(hi.ptr(q), q.stride(0), hi.ptr(kc), hi.ptr(kc), 1 << 25, hi.ptr(out), out.stride(0),
+                                 4, 0, 2, 1, 64, hi.cur_stream())
+    assert rc == -1, rc
