@@ -119,9 +119,9 @@ int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s
 
 // First-call autotuning per (M bucket, N, K, SwiGLU, int8) and device, as the reference's
 // gemm_choose (api.cu:465-552): every valid (tile, split) is timed on the real activations into a
-// scratch output, with the weights streamed cold (below); the three fastest are re-timed and the
-// best kept. Skipped under stream capture
-// and with HIPINFER_GEMM_AUTOTUNE=0 (the model above decides then).
+// scratch output, with the weights streamed cold (below); the three fastest are re-timed in
+// interleaved rounds and the best median kept. Skipped under stream capture and with
+// HIPINFER_GEMM_AUTOTUNE=0 (the model above decides then).
 std::mutex g_tune_mu;
 std::map<std::tuple<int, int, int, int, bool, bool, bool>, Choice> g_tuned;
 
@@ -219,14 +219,20 @@ int gemm_choose(const GemmArgs& g, int epi, bool q8, hipStream_t s, Choice* out,
     }
   }
   if (!rc && !timed.empty()) {
+    // the three fastest are re-timed in three interleaved rounds (a clock ramp or a transient
+    // then touches every finalist alike) and the one with the lowest median kept
     const size_t nfin = std::min<size_t>(3, timed.size());
     std::partial_sort(timed.begin(), timed.begin() + nfin, timed.end(),
                       [](const auto& a, const auto& b) { return a.first < b.first; });
+    constexpr int kRounds = 3;
+    float fin[3][kRounds];
+    for (int r = 0; r < kRounds && !rc; r++)
+      for (size_t f = 0; f < nfin && !rc; f++) rc = time_it(timed[f].second, std::max(nrot, 8), &fin[f][r]);
     float best = 1e30f;
     for (size_t f = 0; f < nfin && !rc; f++) {
-      float us = 0.f;
-      rc = time_it(timed[f].second, std::max(2 * nrot, 8), &us);
-      if (!rc && us < best) {
+      std::sort(fin[f], fin[f] + kRounds);
+      const float us = fin[f][kRounds / 2];
+      if (us < best) {
         best = us;
         *out = timed[f].second;
       }
