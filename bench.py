@@ -674,10 +674,10 @@ def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
 
 
 def prefill_breakdown(csv_path):
-    """Per-kernel time of the last engine prefill in a rocprofv3 kernel trace (`--kernel-trace
-    --output-format csv`) of `bench.py --profile prefill`: the launches after the second-to-last
-    greedy argmax up to the last one (one whole prefill: embed, 32 layers, lm_head, argmax).
-    Prints a markdown table, longest total first."""
+    """Per-kernel time of the last engine prefill (or decode step) in a rocprofv3 kernel trace
+    (`--kernel-trace --output-format csv`) of `bench.py --profile prefill` (or `decode64`): the
+    launches after the second-to-last greedy argmax up to the last one (one whole prefill or
+    step: embed, 32 layers, lm_head, argmax). Prints a markdown table, longest total first."""
     import csv
     with open(csv_path) as f:
         rows = sorted(((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
@@ -691,7 +691,7 @@ def prefill_breakdown(csv_path):
         d[0] += 1
         d[1] += (end - start) / 1e3
     busy = sum(v[1] for v in agg.values())
-    print(f"prefill span (first launch start to last launch end): {span:.1f} us; kernels busy {busy:.1f} us; "
+    print(f"span (first launch start to last launch end): {span:.1f} us; kernels busy {busy:.1f} us; "
           f"{len(seg)} launches")
     print("| kernel | launches | avg us | total us | share of busy |")
     print("|---|---|---|---|---|")
@@ -900,9 +900,9 @@ def main():
     ap.add_argument("--no-step", action="store_true", help="skip the whole decode step (with attention) section")
     ap.add_argument("--no-engine", action="store_true", help="skip the engine prefill / batched decode section")
     ap.add_argument("--prefill-breakdown", metavar="CSV", default=None,
-                    help="(alone) print the per-kernel table of the last prefill in a kernel trace of "
-                         "--profile prefill")
-    ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe", "c4", "prefill", "flash"] +
+                    help="(alone) print the per-kernel table of the last prefill (or decode step) in a kernel "
+                         "trace of --profile prefill (or decode64)")
+    ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe", "c4", "prefill", "flash", "decode64"] +
                     [k + q for k in ("qkv", "o", "gate_up", "down", "lm_head") for q in ("", "8")], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
     args = ap.parse_args()
@@ -933,6 +933,26 @@ def main():
                 hi.flash_prefill(qq, kc, vc, T, 0, HQ, HKV, out=oo)
             torch.cuda.synchronize()
         log("profile run done (flash)")
+        return
+    if args.profile == "decode64":  # engine decode step of 64 sequences at 1024 positions, fp16, graph replays
+        model = Model(torch, hi, q8_too=False)
+        from hipinfer_amd.engine import DecodeStep
+        g = torch.Generator(device="cuda")
+        g.manual_seed(SEED + 21)
+        embed = torch.empty(V, H, dtype=torch.float16, device="cuda").normal_(0.0, 1.0, generator=g)
+        cfg = dict(H=H, Hq=HQ, Hkv=HKV, D=D, I=I, V=V, L=L, eps=1e-5, theta=500000.0)
+        ds = DecodeStep(cfg, engine_weights(model, embed, False), 64, 1024 + 64)
+        for k in ds.kc + ds.vc:
+            k.normal_(0.0, 1.0, generator=g)
+        ds.pos.fill_(1023)
+        ds.step()  # eager: tunes the GEMM tiles
+        torch.cuda.synchronize()
+        gr = ds.capture()
+        ds.pos.fill_(1023)
+        for _ in range(5):
+            gr.replay()
+        torch.cuda.synchronize()
+        log("profile run done (decode64)")
         return
     if args.profile == "prefill":  # engine prefill of a 1024-token prompt, fp16: a tuning call, then 3
         model = Model(torch, hi, q8_too=False)
