@@ -56,6 +56,15 @@ def test_decode_attn(hi, O, D, G):
               2e-3, 1e-2)
 
 
+def test_decode_attn_batch64(hi, O):
+    """The batched decode step's shape (Llama-3.1-8B: Hkv 8, G 4, D 128) at 64 sequences and about
+    1024 positions: one split per (sequence, kv head), so each wave runs four tiles in turn with the
+    next tile's K and V in flight during the current one; ragged lengths end tiles part-way."""
+    lens = [1024 - 13 * i for i in range(64)]
+    got, ref = attn_case(hi, O, lens, 32, 8, 128, 1040, 650)
+    check("decode attn B=64 lens=1024..205", got, ref, 2e-3, 1e-2)
+
+
 def test_decode_work_reuse(hi, O):
     """One zeroed work buffer for launches of decreasing and increasing batch: the split counters
     must be left zeroed and never land in a larger launch's partials. One kv head per sequence
