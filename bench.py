@@ -362,19 +362,26 @@ def capture(torch, fn):
     return g
 
 
-def time_graph(torch, g, steps, warmup):
+def time_graph(torch, g, steps, warmup, full=False):
+    """Replays g `steps` times after `warmup` untimed replays, with a HIP event on the replay stream
+    before the first replay and after each one. Returns the median replay time in ms (the reference
+    reports medians, scripts/bench.py:28-48) and the host wall time per replay; full=True adds the
+    mean (first to last event over steps)."""
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps):
+    ev[0].record()
+    for i in range(steps):
         g.replay()
-    e1.record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3
-    return e0.elapsed_time(e1) / steps, wall / steps
+    med = statistics.median(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    if full:
+        return med, wall / steps, ev[0].elapsed_time(ev[steps]) / steps
+    return med, wall / steps
 
 
 def _cpu_layer(torch, dims, layer, q8_layer, n1, n2, seed):
@@ -504,7 +511,13 @@ def cpu_baseline(torch, model):
                 legs[f"c_{name}_{fmt}_{cores}core"] = {"GB/s": round(nbytes / t / 1e9, 3), "ms": round(t * 1e3, 3),
                                                        "threads": O.get_threads(), "runs": n}
     head = legs["torch_C2_fp16"]
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
     return {"value": head["GB/s"], "unit": "GB/s", "cores": tthreads, "kind": "port",
+            "host_cpus": {"nproc": os.cpu_count(), "affinity": affinity, "job_share": share,
+                          "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")},
             "sample": "one Llama-3.1-8B layer's decode GEMVs (QKV+RoPE, o+res, gate/up+SwiGLU, down+res; "
                       "436.2 MB of fp16 weights, M = 1) through the reference's CPU engine restated in torch "
                       "float32 (scripts/ref_engine.py mm/rmsnorm/swiglu), median of >= 5 runs; legs: the same "
@@ -1000,15 +1013,15 @@ def main():
 
     # ---- the step: one fp16 token through all 32 layers + lm_head
     g16 = capture(torch, lambda: model.token(False))
-    ms16, wall16 = time_graph(torch, g16, args.steps, args.warmup)
+    ms16, wall16, mean16 = time_graph(torch, g16, args.steps, args.warmup, full=True)
     assert torch.isfinite(model.logits).all(), "non-finite logits"
-    out = {"fp16": (ms16, wall16)}
+    out = {"fp16": (ms16, wall16, mean16)}
     kernels = {}
     if model.q8 is not None:
         g8 = capture(torch, lambda: model.token(True))
-        ms8, wall8 = time_graph(torch, g8, args.steps, args.warmup)
+        ms8, wall8, mean8 = time_graph(torch, g8, args.steps, args.warmup, full=True)
         assert torch.isfinite(model.logits).all(), "non-finite logits (int8)"
-        out["int8"] = (ms8, wall8)
+        out["int8"] = (ms8, wall8, mean8)
     # ---- each GEMV kind alone (32 distinct weight sets back to back), fp16 and int8
     for q8 in ([False, True] if model.q8 is not None else [False]):
         for kind in ["qkv", "o", "gate_up", "down", "lm_head"]:
@@ -1043,12 +1056,15 @@ def main():
                                "lm_head, every weight streamed once per token (hipGraph replay)",
                    "weight_bytes_per_step": wb16, "act_bytes_per_step": act_bytes()},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "timing": "ms_per_step is the median replay (HIP events around each replay); mean over all steps beside it",
+        "mean_ms_per_step": round(mean16, 4),
         "wall_ms_per_step": round(wall16, 4),
     }
     if "int8" in out:
         wb8 = weight_bytes(True)
         v8 = wb8 / (out["int8"][0] * 1e-3) / 1e9
         res["int8"] = {"value": round(v8, 1), "unit": "GB/s", "ms_per_step": round(out["int8"][0], 4),
+                       "mean_ms_per_step": round(out["int8"][2], 4),
                        "pct_hbm_peak": round(100 * v8 / HBM_PEAK_GBS, 2), "weight_bytes_per_step": wb8}
     res["kernels"] = kernels
     roofline["traffic"] = traffic_from_profile()

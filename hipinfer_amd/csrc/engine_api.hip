@@ -292,13 +292,43 @@ int moe_rows(Engine* e, const Layer& w, f16* x, f16* xn, int m) {
 
 enum { kGuGemm = 1, kDownGemm = 2, kLmGemm = 4 };
 
-// The projections of a B-sequence decode step (2 <= B <= gemv_max) that run faster on the GEMM
-// path: each of gate/up, down and lm_head is timed both ways on scratch rows (the weights of up
-// to 8 layers in turn, so they stream from HBM as in a step), the GEMM side with the RMSNorm the
-// GEMV fuses; the GEMM must win by 3 %. HIPINFER_SMALL_GEMM=<mask> sets the choice instead.
+// The projections of a B-sequence decode step (2 <= B <= gemv_max) that run on the GEMM path, by a
+// fixed rule on the shapes (from step times measured both ways on Llama-3.1-8B and Qwen2.5-1.5B,
+// fp16 and int8, at 2-8 sequences):
+//  - down, when its B activation rows (K = inter) do not fit one GEMV launch's LDS together (the
+//    GEMV would run in row chunks, each streaming the weights), or with int8 weights from 5 rows
+//    on, where the int8 GEMV's per-row dot products make it instruction-bound;
+//  - lm_head with int8 weights from 5 rows on, for the same reason.
+// gate/up, QKV and o stay on the GEMV. The choice depends only on the model's shapes, its weight
+// format and B, so every process and every box runs the same kernels for a batch size. A row of a
+// B-sequence step whose down or lm_head runs on the GEMM is not bit-identical to a batch-of-one
+// step of that sequence (the verify path keeps the GEMVs for that reason).
+int small_paths_rule(const Engine* e, int B) {
+  const Cfg& c = e->c;
+  if (B < 2) return 0;
+  const bool q8 = e->lm.s != nullptr;
+  int mask = 0;
+  if (!c.moe) {
+    const bool dq8 = e->L[0].down.s != nullptr;
+    const int fit = gemv_rows_per_launch(c.inter, false, dq8);
+    if (B > fit || (dq8 && B >= 5)) mask |= kDownGemm;
+  }
+  if (q8 && B >= 5) mask |= kLmGemm;
+  return mask;
+}
+
+// The same choice made by timing: each of gate/up, down and lm_head is timed both ways on scratch
+// rows (the weights of up to 8 layers in turn, so they stream from HBM as in a step), the GEMM side
+// with the RMSNorm the GEMV fuses; the GEMM must win by 3 %. Used with HIPINFER_SMALL_GEMM=tune;
+// HIPINFER_SMALL_GEMM=<mask> sets the mask; unset, small_paths_rule decides.
 int tune_small_paths(Engine* e, int B, int* mask) {
   if (const char* env = getenv("HIPINFER_SMALL_GEMM")) {
-    *mask = atoi(env) & 7;
+    if (strcmp(env, "tune") != 0) {
+      *mask = atoi(env) & 7;
+      return 0;
+    }
+  } else {
+    *mask = small_paths_rule(e, B);
     return 0;
   }
   const Cfg& c = e->c;
@@ -379,7 +409,7 @@ int decode_step(Engine* e, int B) {
     } else {
       hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
       EN_TRY(hipStreamIsCapturing(s, &cap));
-      if (cap == hipStreamCaptureStatusNone) {  // timed once, eagerly; a capture keeps the GEMVs
+      if (cap == hipStreamCaptureStatusNone) {  // chosen once, eagerly; a capture keeps the GEMVs
         EN_TRY(tune_small_paths(e, B, &sg));
         e->small_gemm[B] = sg;
       }
@@ -706,7 +736,7 @@ HI_EXPORT int hi_prefill(Engine* e, int slot, const int* tokens, int T, int p0) 
   if (hipSetDevice(e->dev) != hipSuccess || prefill(e, slot, tokens, T, p0, nullptr)) return -1;
   int tok = -1;
   if (hipMemcpyAsync(&tok, e->tok + slot, 4, hipMemcpyDeviceToHost, e->st) != hipSuccess ||
-      hipStreamSynchronize(e->st) != hipSuccess)
+      hipStreamSynchronize(e->st) != hipSuccess || (e->c.moe && moe_one_launch_failed()))
     return -1;
   return tok;
 }
@@ -722,7 +752,7 @@ HI_EXPORT int hi_prefill_logits(Engine* e, int slot, const int* tokens, int T, i
   if (hipSetDevice(e->dev) != hipSuccess || prefill(e, slot, tokens, T, p0, (f16*)dst)) return -1;
   int tok = -1;
   if (hipMemcpyAsync(&tok, e->tok + slot, 4, hipMemcpyDeviceToHost, e->st) != hipSuccess ||
-      hipStreamSynchronize(e->st) != hipSuccess)
+      hipStreamSynchronize(e->st) != hipSuccess || (e->c.moe && moe_one_launch_failed()))
     return -1;
   return tok;
 }
@@ -764,6 +794,7 @@ HI_EXPORT float hi_decode(Engine* e, int B, int steps, int use_graph) {
     ok = use_graph ? hipGraphLaunch(e->graphs[B], e->st) == hipSuccess : decode_step(e, B) == 0;
   ok = ok && hipEventRecord(ev[3], e->st) == hipSuccess && hipEventSynchronize(ev[3]) == hipSuccess &&
        hipEventElapsedTime(&part, ev[2], ev[3]) == hipSuccess;
+  if (ok && e->c.moe && moe_one_launch_failed()) ok = false;  // a step's MoE output was wrong
   ms += part;
   for (auto& v : ev) (void)hipEventDestroy(v);
   if (!ok) (void)hipGetLastError();

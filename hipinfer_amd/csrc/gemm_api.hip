@@ -346,7 +346,7 @@ int gemm_entry(const void* A, int lda, const void* W, const void* scales, const 
   if (g_force_splits >= 1) ch.splits = g_force_splits;
   if (!norm_y) return launch_choice(g, ch, epi, q8, s);
   const bool fuse = N <= 8192;
-  if (fuse) {  // set after the choice: the tuner times the plain second pass
+  if (fuse) {  // the tuner timed each candidate with its norm; the norm fields go on g for the final launch only
     g.norm_w = (const f16*)norm_w;
     g.norm_y = (f16*)norm_y;
     g.norm_eps = eps;
@@ -368,11 +368,17 @@ constexpr size_t kScratchBytes = size_t(64) << 20;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 namespace {
+constexpr int kScratchDevices = 64;
 std::mutex g_scratch_mu;
-float* g_scratch[64] = {};
+float* g_scratch[kScratchDevices] = {};
 
 // The current device's copy of `scratch`, looked up once per device (with that device current).
 float* scratch_on(const HiDevice* d) {
+  if (d->id < 0 || d->id >= kScratchDevices) {
+    fprintf(stderr, "hipinfer_amd: hi_gemm_noalloc: device id %d outside the %d devices it keeps scratch for\n", d->id,
+            kScratchDevices);
+    return nullptr;
+  }
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch[d->id]) {
     void* p = nullptr;

@@ -15,6 +15,24 @@ template <> int gemv_run<3>(const GemvArgs&, int, bool, int, hipStream_t);
 
 static bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// LDS per activation row: the row, its per-wave norm partials and inverse RMS, and for int8
+// weights one partial sum per staging thread
+static size_t gemv_row_lds(int K, bool int8) {
+  return (size_t)K * 2 + (kGemvWaves + 1) * sizeof(float) + (int8 ? kGemvThreads * sizeof(float) : 0);
+}
+
+static int rows_per_launch(size_t row_lds, bool norm, int lds_max) {
+  if (row_lds > (size_t)lds_max) return 0;
+  int cap = norm ? 8 : 16;
+  while (cap > 1 && (size_t)cap * row_lds > (size_t)lds_max) cap >>= 1;
+  return cap;
+}
+
+int gemv_rows_per_launch(int K, bool norm, bool int8) {
+  const HiDevice* d = hi_device();
+  return d ? rows_per_launch(gemv_row_lds(K, int8), norm, d->lds_max) : 0;
+}
+
 static int gemv_common(GemvArgs a, int epi, hipStream_t s, const char* who) {
   const HiDevice* d = hi_device();
   if (!d) return -2;
@@ -30,15 +48,9 @@ static int gemv_common(GemvArgs a, int epi, hipStream_t s, const char* who) {
   if (a.scales && !aligned(a.scales, 2)) HI_FAIL("%s: scales must be 2-byte aligned", who);
   const int n_out = epi == 2 ? a.N / 2 : a.N;
   if (epi != 3 && a.ldo < n_out) HI_FAIL("%s: ldo %lld < %d output columns", who, (long long)a.ldo, n_out);
-  // LDS per activation row: the row, its per-wave norm partials and inverse RMS, and for int8
-  // weights one partial sum per staging thread
-  const size_t row_lds =
-      (size_t)a.K * 2 + (kGemvWaves + 1) * sizeof(float) + (wf != WF_F16 ? kGemvThreads * sizeof(float) : 0);
-  if (row_lds > (size_t)d->lds_max) HI_FAIL("%s: K=%d activation row exceeds LDS", who, a.K);
-
   const bool norm = a.normw != nullptr;
-  int cap = norm ? 8 : 16;
-  while (cap > 1 && (size_t)cap * row_lds > (size_t)d->lds_max) cap >>= 1;
+  int cap = rows_per_launch(gemv_row_lds(a.K, wf != WF_F16), norm, d->lds_max);
+  if (!cap) HI_FAIL("%s: K=%d activation row exceeds LDS", who, a.K);
   if (epi == 3) {
     // the fused QKV epilogue writes a launch's cache rows at 32-bit byte offsets from its first
     // slot (and q rows from out): fewer rows per launch when a slot is large

@@ -22,9 +22,12 @@
 //    launches one GEMM per expert, api.cu:901-909) nothing returns to the host, so the grouped
 //    path is graph-capturable too.
 // Expert ids outside [0, E) are never dereferenced: such a slot contributes nothing.
+#include <atomic>
 #include <cstdlib>
+#include <mutex>
 
 #include "gemm.h"
+#include "hi_internal.h"
 
 namespace {
 
@@ -539,7 +542,7 @@ template <int CH, int KM, int RND>
 __global__ void __launch_bounds__(kFusedWaves * 64) moe_decode_one_kernel(
     const f16* __restrict__ xn, const f16* __restrict__ Wr, const f16* __restrict__ wgu,
     const f16* __restrict__ wdown, int k, int E, int H, int I, int flags, float scale, int cols_per_block,
-    int* __restrict__ idx_out, float* __restrict__ w_out, uint32_t* act2, f16* x, unsigned* bar) {
+    int* __restrict__ idx_out, float* __restrict__ w_out, uint32_t* act2, f16* x, unsigned* bar, int* fail) {
   __shared__ float logit[kMoeMaxE];
   __shared__ float selv[kMoeMaxK];
   __shared__ int seli[kMoeMaxK];
@@ -640,15 +643,22 @@ __global__ void __launch_bounds__(kFusedWaves * 64) moe_decode_one_kernel(
     }
   }
   // every block waits for every arrival (all blocks are resident, so every wait ends; the poll
-  // count is bounded all the same)
+  // count is bounded all the same). A block whose polls run out goes on, so the grid still drains,
+  // and raises the host-visible fail word: its output is wrong, and the host reports it on the next
+  // MoE call or engine step and stops using this path.
   if (wave == kPoller) {
     // one poll in flight: a second one (checked while the next is out) measured slower, the
     // counters' memory channel serving the polls and the arrivals alike
+    bool arrived = false;
     for (int it = 0; it < kMoeSpinMax; it++) {
       const bool ok = lane >= 8 || (int)(ld_coherent_u32(&bar[lane * kMoeBarStride]) - target) >= 0;
-      if (__all(ok)) break;
+      if (__all(ok)) {
+        arrived = true;
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
     }
+    if (!arrived && lane == 0) __hip_atomic_store(fail, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     if (blockIdx.x == 0 && lane < 8) __hip_atomic_store(&bar[8 * kMoeBarStride + lane], target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
@@ -699,6 +709,30 @@ __global__ void __launch_bounds__(kFusedWaves * 64) moe_decode_one_kernel(
   }
 }
 
+// The one-launch kernel's fail word: one pinned host int (mapped for the GPU, so a kernel's
+// system-scope store reaches the host without a copy), allocated on the first one-launch call made
+// outside stream capture. Raised by a block whose handoff wait ran out of polls; taken (read and
+// cleared) by moe_one_launch_failed, which also turns the one-launch path off for the process.
+std::mutex g_moe_fail_mu;
+int* g_moe_fail = nullptr;
+std::atomic<bool> g_moe_one_off{false};
+
+int* moe_fail_word(hipStream_t st) {
+  std::lock_guard<std::mutex> lk(g_moe_fail_mu);
+  if (!g_moe_fail) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+    void* p = nullptr;
+    if (hipHostMalloc(&p, sizeof(int), hipHostMallocDefault) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    __atomic_store_n((int*)p, 0, __ATOMIC_RELEASE);
+    g_moe_fail = (int*)p;
+  }
+  return g_moe_fail;
+}
+
 // Launches moe_decode_one_kernel for one token when its grid can be resident all at once: k * I / 16
 // blocks of 16 waves (each 16 gate/up units, then up to 16 down columns). Returns 0 after the
 // launch, 1 when the shape or the occupancy does not allow it (the caller takes the two launches),
@@ -713,8 +747,10 @@ int moe_decode_one_go(const void* xn, const void* Wr, const void* wgu, const voi
   const int bpc = hi_blocks_per_cu(reinterpret_cast<const void*>(fn), kFusedWaves * 64, 0);
   if (bpc < 0) return -2;
   if ((long)bpc * d->cus < nb) return 1;  // not resident at once: the handoff could not be waited for
+  int* fail = moe_fail_word(st);
+  if (!fail) return 1;  // no fail word (a capture before the first eager call): the two launches
   hipLaunchKernelGGL(fn, dim3(nb), dim3(kFusedWaves * 64), 0, st, (const f16*)xn, (const f16*)Wr, (const f16*)wgu,
-                     (const f16*)wdown, k, E, H, I, flags, scale, cpb, idx, w, (uint32_t*)act, (f16*)x, bar);
+                     (const f16*)wdown, k, E, H, I, flags, scale, cpb, idx, w, (uint32_t*)act, (f16*)x, bar, fail);
   HI_TRY(hipGetLastError());
   return 0;
 }
@@ -740,7 +776,7 @@ bool moe_one_launch_enabled() {
     const char* e = getenv("HIPINFER_MOE_ONE_LAUNCH");
     return !e || atoi(e) != 0;
   }();
-  return on;
+  return on && !g_moe_one_off.load();
 }
 
 int moe_decode_one(const void* xn, const void* Wr, const void* wgu, const void* wdown, int E, int k, int H, int I,
@@ -763,6 +799,17 @@ int moe_decode_one(const void* xn, const void* Wr, const void* wgu, const void* 
 }
 
 }  // namespace
+
+bool moe_one_launch_failed() {
+  std::lock_guard<std::mutex> lk(g_moe_fail_mu);
+  if (!g_moe_fail || __atomic_load_n(g_moe_fail, __ATOMIC_ACQUIRE) == 0) return false;
+  __atomic_store_n(g_moe_fail, 0, __ATOMIC_RELEASE);
+  g_moe_one_off.store(true);
+  fprintf(stderr,
+          "hipinfer_amd: a one-launch MoE call gave up waiting for its grid (its blocks were not all resident "
+          "at once): that call's output is wrong; the one-launch path is off for the rest of this process\n");
+  return true;
+}
 
 // Router + top-k for M normalised rows xn: idx[M, k] (int) and weights w[M, k] (fp32), descending.
 HI_EXPORT int hi_moe_router(const void* xn, int ldx, const void* Wr, int M, int E, int H, int k, int flags, int* idx,
@@ -868,6 +915,7 @@ HI_EXPORT int hi_moe_route_experts(const void* xn, int ldxn, const void* Wr, con
   if (((uintptr_t)xn & 15) || ((uintptr_t)Wr & 15) || ((uintptr_t)wgu & 15) || ((uintptr_t)wdown & 15) ||
       ((uintptr_t)x & 15) || ((uintptr_t)work & 255) || ldxn % 8 || ldx % 8)
     HI_FAIL("hi_moe_route_experts: tensors must be 16-byte aligned (work 256-byte), ldxn and ldx multiples of 8");
+  if (moe_one_launch_failed()) return -2;  // an earlier call's output was wrong: report it, launch nothing
   const hipStream_t st = (hipStream_t)s;
   const int n = M * k;
   const MoeWork wk = moe_work(work, n, E, H);

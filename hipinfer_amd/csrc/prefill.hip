@@ -291,26 +291,35 @@ __global__ void __launch_bounds__(128 * RG)
   }
 }
 
-// One qkv row per block: q heads rotated in place, rotated k and raw v to the cache.
-__global__ void __launch_bounds__(256)
-    rope_cache_kernel(f16* qkv, int64_t ldq, int Hq, int Hkv, int D, const f16x2* __restrict__ cs,
-                      const int* __restrict__ pos, int pos_base, int slot_base, f16* kc, f16* vc, int max_seq) {
-  const int HD = D / 2, row = blockIdx.x;
-  const int p = pos ? pos[row] : pos_base + row;
-  const int slot = pos ? slot_base + row : slot_base;
-  f16* base = qkv + (int64_t)row * ldq;
-  for (int i = threadIdx.x; i < (Hq + Hkv) * HD; i += blockDim.x) {
-    const int hh = i / HD, d = i % HD;
-    f16* x = base + hh * D;
-    f16 y1 = x[d], y2 = x[d + HD];
-    rope_pair(y1, y2, cs[(int64_t)p * HD + d]);
-    f16* dst = hh < Hq ? x : kc + (((int64_t)slot * Hkv + hh - Hq) * max_seq + p) * D;
-    dst[d] = y1;
-    dst[d + HD] = y2;
+// Any alignment (2-byte accesses only): block (row, head group), one wave per head of the row's
+// Hq + 2 Hkv heads. A q head is rotated in place, a k head rotated into the cache, a v head copied
+// into the cache; lane j takes the pairs (j, j + D/2), (j + 64, j + 64 + D/2), ... of its head.
+// Each pair goes through rope_pair, as in the 16-byte kernel below, so both give the same bits.
+constexpr int kRopeHeadsPerBlock = 4;
+
+__global__ void __launch_bounds__(64 * kRopeHeadsPerBlock)
+    rope_cache_heads_kernel(f16* qkv, int64_t ldq, int Hq, int Hkv, int D, const f16x2* __restrict__ cs,
+                            const int* __restrict__ pos, int pos_base, int slot_base, f16* kc, f16* vc, int max_seq) {
+  const int r = blockIdx.x, lane = threadIdx.x & 63;
+  const int head = blockIdx.y * kRopeHeadsPerBlock + (threadIdx.x >> 6);
+  if (head >= Hq + 2 * Hkv) return;
+  const int at = pos ? pos[r] : pos_base + r;                  // position in the cache
+  const int64_t cslot = pos ? (int64_t)slot_base + r : slot_base;
+  f16* src = qkv + (int64_t)r * ldq + (int64_t)head * D;
+  if (head >= Hq + Hkv) {
+    f16* dst = vc + ((cslot * Hkv + (head - Hq - Hkv)) * max_seq + at) * D;
+    for (int e = lane; e < D; e += 64) dst[e] = src[e];
+    return;
   }
-  const f16* v = base + (Hq + Hkv) * D;
-  for (int i = threadIdx.x; i < Hkv * D; i += blockDim.x)
-    vc[(((int64_t)slot * Hkv + i / D) * max_seq + p) * D + i % D] = v[i];
+  f16* dst = head < Hq ? src : kc + ((cslot * Hkv + (head - Hq)) * max_seq + at) * D;
+  const int half = D >> 1;
+  const f16x2* tab = cs + (int64_t)at * half;
+  for (int j = lane; j < half; j += 64) {
+    f16 lo = src[j], hi = src[j + half];
+    rope_pair(lo, hi, tab[j]);
+    dst[j] = lo;
+    dst[j + half] = hi;
+  }
 }
 
 // The same with 16-byte accesses: a thread step rotates 8 pairs of one head (the 8 elements at d
@@ -394,12 +403,19 @@ HI_EXPORT int hi_rope_cache(void* qkv, int ldq, int M, int Hq, int Hkv, int D, c
   if (M == 0) return 0;
   if (!qkv || !cs || !kc || !vc) HI_FAIL("hi_rope_cache: null tensor pointer");
   if (ldq < (Hq + 2 * Hkv) * D) HI_FAIL("hi_rope_cache: ldq %d < (Hq + 2 Hkv) D", ldq);
+  if ((Hq + 2 * Hkv + kRopeHeadsPerBlock - 1) / kRopeHeadsPerBlock > 65535)
+    HI_FAIL("hi_rope_cache: %d heads per row exceed the launch grid", Hq + 2 * Hkv);
   if (!pos && (pos_base < 0 || (int64_t)pos_base + M > max_seq))
     HI_FAIL("hi_rope_cache: positions %d..%d outside the cache (max_seq %d)", pos_base, pos_base + M - 1, max_seq);
   if (!aligned(cs, 4)) HI_FAIL("hi_rope_cache: cs must be 4-byte aligned");
   const bool v8 = D % 16 == 0 && ldq % 8 == 0 && aligned(qkv, 16) && aligned(cs, 16) && aligned(kc, 16) && aligned(vc, 16);
-  hipLaunchKernelGGL(v8 ? rope_cache_v8_kernel : rope_cache_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, (f16*)qkv,
-                     (int64_t)ldq, Hq, Hkv, D, (const f16x2*)cs, pos, pos_base, slot_base, (f16*)kc, (f16*)vc, max_seq);
+  if (v8)
+    hipLaunchKernelGGL(rope_cache_v8_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, (f16*)qkv, (int64_t)ldq, Hq, Hkv,
+                       D, (const f16x2*)cs, pos, pos_base, slot_base, (f16*)kc, (f16*)vc, max_seq);
+  else
+    hipLaunchKernelGGL(rope_cache_heads_kernel, dim3(M, (Hq + 2 * Hkv + kRopeHeadsPerBlock - 1) / kRopeHeadsPerBlock),
+                       dim3(64 * kRopeHeadsPerBlock), 0, (hipStream_t)stream, (f16*)qkv, (int64_t)ldq, Hq, Hkv, D,
+                       (const f16x2*)cs, pos, pos_base, slot_base, (f16*)kc, (f16*)vc, max_seq);
   HI_TRY(hipGetLastError());
   return 0;
 }

@@ -56,15 +56,19 @@ class DecodeStep:
     "n1", "n2": [H]}]} with gate/up rows interleaved in groups of 16 (export.py:97-101).
     B: cache slots = sequences per decode step (1..64); max_prefill: rows per prefill chunk (0: no
     prefill buffers); small_gemm: for 2..8 sequences, the mask of projections (GU_GEMM, DOWN_GEMM,
-    LM_GEMM) to run on the GEMM path, or None to time them on the first eager step (the
-    HIPINFER_SMALL_GEMM environment variable, when set, gives the mask instead)."""
+    LM_GEMM) to run on the GEMM path, or None for the library engine's shape rule
+    (small_paths_rule); the HIPINFER_SMALL_GEMM environment variable, when set, gives the mask
+    instead, or with the value "tune" times both paths on the first eager step."""
 
     def __init__(self, cfg, weights, B, max_seq, max_prefill=0, small_gemm=None):
         assert 1 <= B <= GEMM_MAX, f"1..{GEMM_MAX} sequences per decode step"
         self.c, self.w, self.B, self.max_seq = dict(cfg), weights, B, max_seq
         self.gemm_path = B > GEMV_MAX
-        if small_gemm is None and os.environ.get("HIPINFER_SMALL_GEMM"):
-            small_gemm = int(os.environ["HIPINFER_SMALL_GEMM"]) & 7
+        env = os.environ.get("HIPINFER_SMALL_GEMM")
+        if small_gemm is None and env and env != "tune":
+            small_gemm = int(env) & 7
+        if small_gemm is None and env != "tune":
+            small_gemm = self.small_paths_rule(cfg, weights, B)
         self.small_gemm = 0 if (B == 1 or self.gemm_path) else small_gemm  # None: not timed yet
         H, Hq, Hkv, D, I, V, L = (cfg[k] for k in ("H", "Hq", "Hkv", "D", "I", "V", "L"))
         self.qkv_dim = (Hq + 2 * Hkv) * D
@@ -111,6 +115,30 @@ class DecodeStep:
         hi.gemm(xn, Wg, out=act, epi=2, scales=sg)
         Wd, sd = self._ws(ly["down"])
         hi.gemm_rmsnorm(act, Wd, x, next_norm, eps, out=xn, scales=sd)
+
+    @staticmethod
+    def small_paths_rule(cfg, weights, B):
+        """The projections of a B-sequence GEMV-path step that run on the GEMM, by the library
+        engine's fixed shape rule (engine_api.hip small_paths_rule): down when its B activation rows
+        do not fit one GEMV launch's LDS (the launch would run in row chunks) or, with int8 weights,
+        from 5 rows on; lm_head with int8 weights from 5 rows on. gate/up, QKV and o stay on the
+        GEMV."""
+        if B < 2:
+            return 0
+        lds = hi.lib.hi_max_smem()
+        mask = 0
+        dq8 = isinstance(weights["layers"][0]["down"], tuple)
+        # LDS per activation row of a GEMV launch (8 waves of 64): the row, 9 floats of norm
+        # partials and inverse RMS, and with int8 weights one float per staging thread
+        row = cfg["I"] * 2 + 9 * 4 + (512 * 4 if dq8 else 0)
+        fit = 16
+        while fit > 1 and fit * row > lds:
+            fit //= 2
+        if row > lds or B > fit or (dq8 and B >= 5):
+            mask |= DOWN_GEMM
+        if isinstance(weights["lm"], tuple) and B >= 5:
+            mask |= LM_GEMM
+        return mask
 
     def _tune_small_paths(self, eps):
         """Time gate/up, down and lm_head on the GEMV path and on the GEMM path (with the RMSNorm

@@ -217,7 +217,7 @@ int hi_rewind(Engine* e, int slot, int len, int tok);
 void hi_sync(Engine* e);
 /* The engine's hipStream_t. Replaces api.cu:2178. */
 void* hi_stream(Engine* e);
-/* Rows per hi_verify call (k + 1 for k draft tokens): 8. Replaces api.cu:2070. */
+/* Rows per hi_verify call (k + 1 for k draft tokens): 16 (the reference returns 8). Replaces api.cu:2070. */
 int hi_verify_max_rows(void);
 /* Speculative verification of a dense model: the greedy token after each of R host tokens fed at
  * positions p0.. of `slot`, through a batch-of-one decode step's kernels with R rows, so entry i

@@ -85,11 +85,11 @@ def oracle_step(O, c, Wd, tok, pos, kc, vc, cs):
     return logits, O.argmax(logits)
 
 
-@pytest.mark.parametrize("mask", [None, 7, 2], ids=["timed_paths", "gemm_gu_down_lm", "gemm_down"])
+@pytest.mark.parametrize("mask", [None, 7, 2], ids=["rule_paths", "gemm_gu_down_lm", "gemm_down"])
 @pytest.mark.parametrize("q8", [False, True], ids=["fp16", "int8"])
 def test_decode_step_vs_oracle_chain(hi, O, q8, mask):
     """mask: the projections a 2-sequence step runs on the GEMM path (engine.GU_GEMM | DOWN_GEMM |
-    LM_GEMM), or None for the choice the first step times; every choice must match the oracle."""
+    LM_GEMM), or None for the engine's shape rule; every choice must match the oracle."""
     import torch
     from hipinfer_amd.engine import DecodeStep
     r = rng(800 + q8)

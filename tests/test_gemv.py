@@ -370,6 +370,38 @@ def test_llama31_8b_lm_head(hi, O, q):
 
 
 @pytest.mark.parametrize("q", [False, True], ids=["fp16", "int8"])
+def test_llama31_8b_o_and_down(hi, O, q):
+    """C2's two residual GEMVs at full size, o_proj 4096 -> 4096 and down 14336 -> 4096, called as
+    the decode token calls them (epi 1 into the residual stream, the launch shape the host picks for
+    N = 4096 at 1 and 8 rows). Every output column is checked against the oracle on the same bytes,
+    and row m of the 8-row call must equal the 1-row call of that row bit for bit."""
+    r = rng(60 + q)
+    H, I = 4096, 14336
+    kind = "int8" if q else "fp16"
+    for name, K, seed in [("o_proj", H, 60), ("down", I, 61)]:
+        Wd, sd = gpu_weights(hi, seed, H, K, q)
+        Wh, sh = host(Wd), None if sd is None else host(sd)
+        x = h16(r, 8, K)
+        if name == "down":  # SwiGLU outputs: small, mostly positive-skewed values
+            x = (x * 0.25).astype(np.float16)
+        res = h16(r, 8, H)
+        ones = []
+        for m in range(8):
+            out = cuda(res[m:m + 1])
+            hi.gemv(cuda(x[m:m + 1]), Wd, out=out, epi=1, scales=sd)
+            ones.append(host(out)[0])
+            if m == 0:
+                ref = O.gemv(x[:1], Wh, out=res[:1].copy(), epi=1, scales=sh)
+                check(f"C2 {name} {kind} M=1", host(out), ref, 4e-3, 2e-3)
+        out = cuda(res)
+        hi.gemv(cuda(x), Wd, out=out, epi=1, scales=sd)
+        got = host(out)
+        check(f"C2 {name} {kind} M=8", got, O.gemv(x, Wh, out=res.copy(), epi=1, scales=sh), 4e-3, 2e-3)
+        for m in range(8):
+            assert np.array_equal(bits(got[m]), bits(ones[m])), f"C2 {name} {kind}: row {m} of 8 differs from the 1-row call"
+
+
+@pytest.mark.parametrize("q", [False, True], ids=["fp16", "int8"])
 def test_qwen25_1p5b_shapes(hi, O, q):
     """C4 (Qwen2.5-1.5B) at the batch / verify widths N = 1, 2, 5, 8: fused-norm gate/up + SwiGLU
     1536 -> 2 x 8960, down + residual 8960 -> 1536, fused-norm QKV + bias + RoPE 1536 -> 2048 (12 q

@@ -190,7 +190,7 @@ def test_engine_from_weight_file_vs_oracle_chain(hi, O, tmp_path, kind, monkeypa
         e.prefill(1, Bp)
         ref_lg1, ref_tok1 = o_prefill(O, ov, Bp, 0, 1, kc, vc, cs)
         e.set_state([t, ref_tok1], [pos, 10])
-        # the two-slot step's gate/up, down and lm_head: the timed choice (dense_bias, moe), or all
+        # the two-slot step's gate/up, down and lm_head: the shape rule's choice (dense_bias, moe), or all
         # three forced onto the GEMM path (tied, int8)
         if kind in ("tied", "int8"):
             monkeypatch.setenv("HIPINFER_SMALL_GEMM", "7")

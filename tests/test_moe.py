@@ -228,3 +228,42 @@ def test_moe_route_experts_rejects_bad_arguments(hi):
         hi.moe_route_experts(xn, Wr, wgu, wdn, 5, xn.clone(), 1)  # k > E
     with pytest.raises(ValueError):
         hi.moe_route_experts(xn[:, :48], Wr[:, :48], wgu[:, :, :48], wdn[:, :48], 2, xn[:, :48].clone(), 1)  # H = 48
+
+
+def test_moe_one_launch_timeout_is_reported(hi):
+    """The one-launch path's bounded handoff wait, made to run out from the host: a zeroed work
+    buffer whose expected-total words (the 8 words after the 8 arrival counters, 256 bytes apart)
+    are preset far above the counters, so no block ever sees its target. Every block gives up after
+    its bounded polls and exits (the call and a device synchronize succeed); the next call reports
+    that output as wrong (-2) and launches nothing; later calls take the two launches and equal the
+    router + experts bit for bit. Last in this file: a reported timeout turns the one-launch path
+    off for the rest of the process."""
+    import torch
+    r = rng(470)
+    E, k, H, I, flags, scale = 32, 8, 1024, 512, 3, 0.22
+    Wr, wgu, wdn = cuda(rn(r, E, H, s=0.05)), cuda(rn(r, E, 2 * I, H, s=0.02)), cuda(rn(r, E, H, I, s=0.02))
+    xn, x0 = cuda(rn(r, 1, H)), cuda(rn(r, 1, H))
+    idx = torch.empty(1, k, dtype=torch.int32, device="cuda")
+    w = torch.empty(1, k, dtype=torch.float32, device="cuda")
+    work = torch.zeros(hi.lib.hi_moe_work_bytes(1, k, E, H, I), dtype=torch.uint8, device="cuda")
+
+    def call(x):
+        return hi.lib.hi_moe_route_experts(hi.ptr(xn), H, hi.ptr(Wr), hi.ptr(wgu), hi.ptr(wdn), 1, E, k, H, I, flags,
+                                           scale, hi.ptr(x), H, hi.ptr(idx), hi.ptr(w), hi.ptr(work), hi.cur_stream())
+
+    assert call(x0.clone()) == 0  # the fail word is allocated on this first, ordinary call
+    torch.cuda.synchronize()
+    work.zero_()
+    work.view(torch.int32)[8 * 64:8 * 64 + 8] = 1 << 20  # expected totals far above the zero counters
+    print("moe one-launch: forcing the bounded handoff wait to run out", flush=True)
+    assert call(x0.clone()) == 0
+    torch.cuda.synchronize()  # every block gave up and exited
+    assert call(x0.clone()) == -2, "the timed-out call was not reported"
+    work.zero_()
+    idx2, w2 = hi.moe_router(xn, Wr, k, flags)
+    ref = host(hi.moe_experts(xn, wgu, wdn, idx2, w2, x0.clone(), flags, scale, 0))
+    for _ in range(2):
+        x = x0.clone()
+        assert call(x) == 0
+        assert np.array_equal(host(idx), host(idx2))
+        assert np.array_equal(host(x).view(np.uint16), ref.view(np.uint16))

@@ -60,6 +60,40 @@ def test_rope_cache(hi, O, D, Hq, Hkv):
     assert np.array_equal(bits(host(dk)), bits(kc)) and np.array_equal(bits(host(dv)), bits(vc)), "cache (decode form)"
 
 
+@pytest.mark.parametrize("D,Hq,Hkv,pad,offset", [(48, 6, 2, 0, 0), (64, 8, 2, 3, 0), (128, 12, 4, 0, 1),
+                                                  (160, 5, 1, 1, 0), (2, 3, 3, 0, 0)],
+                         ids=["D48", "odd-ldq", "unaligned-ptr", "D160", "D2"])
+def test_rope_cache_any_alignment(hi, O, D, Hq, Hkv, pad, offset):
+    """The 2-byte kernel runs whenever the 16-byte one cannot: D % 16 != 0 (D = 48, 160 with 80
+    pairs per head so lanes take two, the minimum D = 2), ldq % 8 != 0 (padded rows), or a qkv
+    pointer that is not 16-byte aligned. Same bits as the oracle, in both the prefill and the
+    decode forms; the row padding stays untouched."""
+    r = rng(1300 + D + pad + offset)
+    S, T, p0 = 256, 19, 60
+    cs = rope_table(S, D)
+    W = (Hq + 2 * Hkv) * D + pad
+    for form in ["prefill", "decode"]:
+        M = T if form == "prefill" else 4
+        flat = r.standard_normal(M * W + offset).astype(np.float16)
+        qkv = flat[offset:].reshape(M, W).copy()
+        kc = np.zeros((M + 3, Hkv, S, D), np.float16)
+        vc = np.zeros_like(kc)
+        dflat, dk, dv = cuda(flat), cuda(kc), cuda(vc)
+        dq = dflat[offset:].view(M, W)
+        if form == "prefill":
+            hi.rope_cache(dq, Hq, Hkv, cuda(cs), dk, dv, pos_base=p0, slot_base=2)
+            O.rope_cache(qkv, Hq, Hkv, cs, kc, vc, pos_base=p0, slot_base=2)
+        else:
+            pos = np.array([0, S - 1, 7, 100], np.int32)
+            hi.rope_cache(dq, Hq, Hkv, cuda(cs), dk, dv, pos=cuda(pos), slot_base=1)
+            O.rope_cache(qkv, Hq, Hkv, cs, kc, vc, pos=pos, slot_base=1)
+        got = host(dflat)
+        assert np.array_equal(bits(got[:offset]), bits(flat[:offset])), "wrote before the rows"
+        assert np.array_equal(bits(got[offset:].reshape(M, W)), bits(qkv)), f"q rotation ({form} form)"
+        assert np.array_equal(bits(host(dk)), bits(kc)), f"k cache ({form} form)"
+        assert np.array_equal(bits(host(dv)), bits(vc)), f"v cache ({form} form)"
+
+
 FP_HEADS = [(64, 32, 4), (64, 32, 8), (128, 24, 8), (128, 16, 16), (128, 28, 4)]
 FP_LENS = [(1, 0), (64, 0), (100, 0), (517, 0), (1024, 0), (70, 300), (33, 1000)]
 
