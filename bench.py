@@ -606,8 +606,9 @@ def moe_bench(torch, hi, steps, seed):
     """Granite-3.1-1B-A400M-shaped MoE layers (hidden 1024, 32 experts of SwiGLU 1024 -> 2 x 512 and
     512 -> 1024, top-8, softmax over the top-8 logits, fp16 routing weights, residual scale 0.22) over
     24 distinct layers: B = 1 decode as the reference's two calls (router, then GEMV experts) and as
-    this library's one call (router inside the gate/up launch), and a 256-token prefill (router +
-    grouped MFMA experts)."""
+    this library's one call (one launch), and a 256-token prefill as the reference's two calls
+    (router, then the grouped MFMA experts: sort, two GEMMs, combine) and as the one call (the sort
+    inside the router's launch)."""
     H, E, I, k, L = 1024, 32, 512, 8, 24
     flags = hi.MOE_NORM_TOPK | hi.MOE_FP16_WEIGHTS
     g = _seeded(torch, seed)
@@ -616,7 +617,8 @@ def moe_bench(torch, hi, steps, seed):
     wdn = [torch.empty(E, H, I, dtype=torch.float16, device="cuda").normal_(0, 0.02, generator=g) for _ in range(L)]
     res = {"config": "Granite-3.1-1B-A400M MoE layer: H 1024, 32 experts (gate/up 1024->2x512, down 512->1024), "
                      "top-8, 24 distinct layers per step"}
-    for M, path, tag in [(1, 1, "decode_B1_gemv"), (1, -1, "decode_B1_fused"), (256, 2, "prefill_256_grouped")]:
+    for M, path, tag in [(1, 1, "decode_B1_gemv"), (1, -1, "decode_B1_fused"), (256, 2, "prefill_256_grouped"),
+                         (256, -1, "prefill_256_fused")]:
         xn = torch.randn(M, H, generator=g, device="cuda").half()
         x0 = torch.randn(M, H, generator=g, device="cuda").half()
         x = x0.clone()
@@ -645,8 +647,12 @@ def moe_bench(torch, hi, steps, seed):
                         "GB/s": round(b / us / 1e3, 1), "pct_hbm_peak": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 1)}
         else:
             flops = 2.0 * M * k * (2 * I * H + H * I) + 2.0 * M * E * H
+            # every expert's weights and the router once, xn read, x read and written, the pairs'
+            # activations (I) and down outputs (H) written and read once each
+            b = E * (2 * I * H + H * I) * 2 + E * H * 2 + 3 * M * H * 2 + 2 * M * k * (I + H) * 2
             res[tag] = {"us_per_layer": round(us, 2), "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1),
-                        "expert_pairs": M * k}
+                        "expert_pairs": M * k, "bytes_per_layer": b, "GB/s": round(b / us / 1e3, 1),
+                        "pct_hbm_peak": round(100 * b / us / 1e3 / HBM_PEAK_GBS, 1)}
     del Wr, wgu, wdn
     torch.cuda.empty_cache()
     return res

@@ -57,13 +57,19 @@ struct GemmArgs {
   int kt_per_split;    // K tiles per split (gridDim.y splits)
   float* ws;           // split-K partials: [splits][M][N] fp32
   bool vec_c;          // C (and the residual read) allow 8-byte accesses: C 8-byte aligned, ldc % 4 == 0
-  // grouped mode (MoE experts): group e owns A/C rows [grp_off[e], grp_off[e+1]) and the weights
-  // at W + e * grp_wstride bytes; its row tiles are [grp_tiles[e], grp_tiles[e+1]) of the global
-  // row-tile count (block id / column tiles)
+  // grouped mode (MoE experts): group e owns sorted rows [grp_off[e], grp_off[e+1]) and the
+  // weights at W + e * grp_wstride bytes; its row tiles are [grp_tiles[e], grp_tiles[e+1]) of the
+  // global row-tile count (block id / column tiles). Sorted row q is A row q and C row q, unless
+  // grp_perm is given: then with grp_gather A row q is A row grp_perm[q] / grp_k (A has
+  // grp_a_rows rows; rows are gathered by the tile DMA itself), and with grp_scatter C row q is
+  // C row grp_perm[q]
   const int* grp_off;
   const int* grp_tiles;
   int grp_n;
   int64_t grp_wstride;
+  const int* grp_perm;
+  int grp_k, grp_a_rows;
+  bool grp_gather, grp_scatter;
   // epilogue 1 with split-K only: the second pass also writes norm_y = RMSNorm(C) * norm_w (rows
   // of N <= 8192 halves, C and norm_y contiguous: ldc == N); nullptr: the plain second pass
   const f16* norm_w;
@@ -72,6 +78,7 @@ struct GemmArgs {
 };
 
 constexpr int kGemmBK = 64;
+constexpr int kGemmMaxGroups = 256;  // grouped mode: at most this many groups (MoE experts)
 // Wait until every LDS read of this wave has returned.
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 // Workgroup barrier without a memory fence (a fence would drain every in-flight LDS DMA); the
@@ -169,24 +176,35 @@ __global__ void __launch_bounds__(64 * WM * WN * KG) gemm_kernel(GemmArgs g) {
   const char* Wb = reinterpret_cast<const char*>(g.W);
   const int tiles_n = (N + BN - 1) / BN;
   int tm, tn, ntiles;
+  [[maybe_unused]] int grp_r0 = 0;  // grouped mode: the group's first sorted row
   if constexpr (GRP) {
-    // find this block's group: grp_tiles[e] <= row tile < grp_tiles[e + 1]; blocks past the last
-    // row tile (the grid is sized for the worst case) exit
-    const int mt = blockIdx.x / tiles_n;
+    // find this block's group: grp_tiles[e] <= row tile < grp_tiles[e + 1] (the prefix is
+    // non-decreasing, so e is the number of groups whose tiles start at or before the row tile,
+    // minus one); blocks past the last row tile (the grid is sized for the worst case) exit. Every
+    // thread loads one group's tile start and first row at once (thread 0 also the totals): one
+    // memory round trip, then one counting barrier.
+    static_assert(64 * NW * KG >= kGemmMaxGroups, "one thread per group");
+    __shared__ int s_tiles[kGemmMaxGroups + 1], s_off[kGemmMaxGroups + 1];
+    const int E = g.grp_n, mt = blockIdx.x / tiles_n;
     tn = blockIdx.x - mt * tiles_n;
-    if (mt >= g.grp_tiles[g.grp_n]) return;
-    int lo = 0, hi = g.grp_n;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (g.grp_tiles[mid] <= mt) lo = mid;
-      else hi = mid;
+    int te = 0;
+    if (tid < E) {
+      te = g.grp_tiles[tid];
+      s_tiles[tid] = te;
+      s_off[tid] = g.grp_off[tid];
     }
-    const int r0 = g.grp_off[lo];
-    M = g.grp_off[lo + 1] - r0;
-    Ap += r0 * g.lda;
-    Cp += r0 * g.ldc;
+    if (tid == 0) {
+      s_tiles[E] = g.grp_tiles[E];
+      s_off[E] = g.grp_off[E];
+    }
+    const int lo = __syncthreads_count(tid < E && te <= mt) - 1;
+    if (mt >= s_tiles[E]) return;
+    grp_r0 = s_off[lo];
+    M = s_off[lo + 1] - grp_r0;
+    if (!g.grp_gather) Ap += grp_r0 * g.lda;
+    if (!g.grp_scatter) Cp += grp_r0 * g.ldc;
     Wb += lo * g.grp_wstride;
-    tm = mt - g.grp_tiles[lo];
+    tm = mt - s_tiles[lo];
     ntiles = 0;
   } else {
     const int tiles_m = (M + BM - 1) / BM;
@@ -218,9 +236,11 @@ __global__ void __launch_bounds__(64 * WM * WN * KG) gemm_kernel(GemmArgs g) {
   //      the rows that exist: rows past M or N read zeros (never stored). Chunks past K (the second
   //      half of a half tile) read bytes of the next row or zeros, and are never used.
   const int valid_m = min(M - bm, BM), valid_n = min(N - bn, BN);
+  const bool gather = GRP && g.grp_gather;  // A rows through grp_perm: the resource spans all of A
+  const int a_bytes = gather ? (int)(((int64_t)(g.grp_a_rows - 1) * g.lda + K) * 2)
+                             : (int)(((int64_t)(valid_m - 1) * g.lda + K) * 2);
   const __amdgpu_buffer_rsrc_t a_rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<f16*>(Ap + (int64_t)bm * g.lda), (short)0, (int)(((int64_t)(valid_m - 1) * g.lda + K) * 2),
-      0x00020000);
+      const_cast<f16*>(gather ? Ap : Ap + (int64_t)bm * g.lda), (short)0, a_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t b_rs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<char*>(Wb + (int64_t)bn * K * (Q8 ? 1 : 2)), (short)0, (int)((int64_t)valid_n * K * (Q8 ? 1 : 2)),
       0x00020000);
@@ -242,15 +262,30 @@ __global__ void __launch_bounds__(64 * WM * WN * KG) gemm_kernel(GemmArgs g) {
       b_lo[par] = a_r * K * 2 + ((a_p ^ sw) << 4);
     }
   }
+  // grouped gather: this lane's row of each A instruction is sorted row grp_r0 + bm + ri + a_r,
+  // fetched from A row grp_perm[that] / grp_k; rows past the group's count get an offset past the
+  // resource, so they read zeros
+  int a_go[A_LD];  // set and read in grouped mode only
+  if constexpr (GRP) {
+#pragma unroll
+    for (int i = 0; i < A_LD; i++) {
+      const int ri = (wave * A_LD + i) * RPI, r = bm + ri + a_r;
+      const int lo_i = a_lo[(ri / RPI) % (BK == 128 ? 4 : 2)] - (int)((int64_t)a_r * g.lda * 2);  // the chunk term
+      if (gather)
+        a_go[i] = r < M ? (int)((int64_t)(g.grp_perm[grp_r0 + r] / g.grp_k) * g.lda * 2) + lo_i : a_bytes;
+      else
+        a_go[i] = a_lo[(ri / RPI) % (BK == 128 ? 4 : 2)] + (int)((int64_t)ri * g.lda * 2);
+    }
+  }
   auto issue = [&](int kt, int st) {
     const int k0 = kt * BK;
     f16* as = As + st * A_ST;
 #pragma unroll
     for (int i = 0; i < A_LD; i++) {
       const int ri = (wave * A_LD + i) * RPI;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_void_t*)(as + ri * BK), 16,
-                                               a_lo[(ri / RPI) % (BK == 128 ? 4 : 2)] + (int)((int64_t)ri * g.lda * 2) + k0 * 2, 0, 0,
-                                               0);
+      // (a plain conditional: an `if constexpr` here kept clang from emitting the grouped kernels)
+      const int off = GRP ? a_go[i] : a_lo[(ri / RPI) % (BK == 128 ? 4 : 2)] + (int)((int64_t)ri * g.lda * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (lds_void_t*)(as + ri * BK), 16, off + k0 * 2, 0, 0, 0);
     }
     char* bs = reinterpret_cast<char*>(Bs + st * B_ST);
 #pragma unroll
@@ -267,6 +302,14 @@ __global__ void __launch_bounds__(64 * WM * WN * KG) gemm_kernel(GemmArgs g) {
   };
 
   const int fr = lane & 31, fk = lane >> 5;  // fragment row (or column) and k half
+  // grouped scatter: the C row of each of this lane's fragment rows, requested now so that the
+  // epilogue waits for nothing
+  int c_row[FM];
+#pragma unroll
+  for (int i = 0; i < FM; i++) {
+    const int row = bm + wm * TM + i * 32 + fr;
+    c_row[i] = (GRP && g.grp_scatter && row < M) ? g.grp_perm[grp_r0 + row] : row;
+  }
   f16x2 bsc[FN];                             // int8: the scale of the W row each B fragment reads
 #pragma unroll
   for (int j = 0; j < FN; j++) {
@@ -530,7 +573,7 @@ __global__ void __launch_bounds__(64 * WM * WN * KG) gemm_kernel(GemmArgs g) {
   for (int i = 0; i < FM; i++) {
     const int row = bm + wm * TM + i * 32 + fr;
     if (row >= M) continue;
-    f16* crow = Cp + (int64_t)row * g.ldc;
+    f16* crow = Cp + (int64_t)c_row[i] * g.ldc;
 #pragma unroll
     for (int j = 0; j < FN; j++) {
       const int c0 = bn + wn * TN + j * 32;  // first column of the 32-column MFMA tile
@@ -645,7 +688,11 @@ constexpr bool gemm_cfg_fits(int c, bool q8, int K) {
   return gemm_cfg_ok(c, q8) && (kGemmCfgs[c].bk < 128 || K % 128 == 0) &&
          (kGemmCfgs[c].kg == 1 || (K % kGemmCfgs[c].bk == 0 && (K / kGemmCfgs[c].bk) % kGemmCfgs[c].kg == 0));
 }
-constexpr int kGemmGrpCfg = 3;  // the grouped (MoE expert) GEMM's tile: 64 x 128
+// The grouped (MoE expert) GEMM's tile: 128 x 128, four 64-deep stages (128 KB of LDS, one block
+// per CU). 128 rows hold a whole expert's share of a 256-token prefill (top-8 of 32 experts: about
+// 64 rows each), so each expert's weights are streamed once; a 64-row tile split most experts into
+// two row tiles, each streaming the same weights.
+constexpr int kGrpBM = 128, kGrpBN = 128, kGrpWM = 2, kGrpWN = 2, kGrpStages = 4;  // 64-deep K tiles
 inline size_t gemm_lds_bytes(int cfg, bool q8) {
   const GemmCfg& c = kGemmCfgs[cfg];
   return (size_t)c.kg * c.st * (c.bm * c.bk * 2 + c.bn * (q8 ? c.bk : 2 * c.bk));

@@ -33,7 +33,6 @@ namespace {
 
 constexpr int kMoeMaxE = 256, kMoeMaxK = 16;
 constexpr int kMoeNormTopk = 1, kMoeFp16Weights = 2;
-constexpr int kGrpBM = 64, kGrpBN = 128;  // grouped GEMM tile (gemm config kGemmGrpCfg)
 
 // v beats (best, bi): NaN above numbers; equal values (and NaN vs NaN) go to the lower index
 // (reference argmax_better, kernels.cuh:1886-1890).
@@ -351,87 +350,132 @@ __global__ void __launch_bounds__(kMoeWaves * 64) moe_gemv_down_kernel(const f16
 }
 
 // ------------------------------------------------------------------ grouped path
-// Counting sort of the n (token, slot) pairs by expert (one block): off[E+1] exclusive prefix of
-// the counts, tiles[E+1] prefix of each expert's row tiles of kGrpBM, perm[q] = pair at sorted
-// position q, inv[pair] = q (-1 for an expert id outside [0, E)). The order within an expert
-// follows the LDS atomics; every GEMM row is computed on its own, so it changes no result.
-__global__ void __launch_bounds__(1024) moe_sort_kernel(const int* __restrict__ idx, int n, int E, int* __restrict__ off,
-                                                        int* __restrict__ tiles, int* __restrict__ perm,
-                                                        int* __restrict__ inv) {
+// Counting sort of the n (token, slot) pairs by expert, by one block of kSortThreads: off[E+1] the
+// exclusive prefix of the per-expert counts, tiles[E+1] the same of their row tiles of kGrpBM, perm[q] the pair at sorted position q. Pairs
+// whose expert id lies outside [0, E) are left out. The two prefixes are one wave's scan (four
+// experts a lane); a thread's ids of a pass are requested together. The order within an expert
+// follows the LDS atomics: every GEMM row is computed on its own, so it changes no result.
+constexpr int kSortThreads = 1024;
+__global__ void __launch_bounds__(kSortThreads) moe_sort_kernel(const int* __restrict__ idx, int n, int E,
+                                                                int* __restrict__ off, int* __restrict__ tiles,
+                                                                int* __restrict__ perm) {
   __shared__ int cnt[kMoeMaxE], cur[kMoeMaxE];
-  for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+  const int tid = threadIdx.x;
+  constexpr int P = 4;  // ids a thread requests together
+  for (int e = tid; e < E; e += kSortThreads) cnt[e] = 0;
   __syncthreads();
-  for (int p = threadIdx.x; p < n; p += blockDim.x) {
-    const int e = idx[p];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int s = 0, ts = 0;
-    for (int e = 0; e < E; e++) {
-      off[e] = s;
-      cur[e] = s;
-      tiles[e] = ts;
-      s += cnt[e];
-      ts += (cnt[e] + kGrpBM - 1) / kGrpBM;
+  int ev0[P];  // the ids of the last (for n <= P * kSortThreads: the only) round
+  for (int p0 = 0; p0 < n; p0 += P * kSortThreads) {
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+      const int p = p0 + j * kSortThreads + tid;
+      ev0[j] = p < n ? idx[p] : -1;
     }
-    off[E] = s;
-    tiles[E] = ts;
+#pragma unroll
+    for (int j = 0; j < P; j++)
+      if (ev0[j] >= 0 && ev0[j] < E) atomicAdd(&cnt[ev0[j]], 1);
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < n; p += blockDim.x) {
-    const int e = idx[p];
-    if (e >= 0 && e < E) {
-      const int q = atomicAdd(&cur[e], 1);
-      perm[q] = p;
-      inv[p] = q;
+  if (tid < 64) {
+    static_assert(kMoeMaxE <= 4 * 64, "four experts a lane");
+    int c[4], tl[4], cs = 0, ts = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int e = 4 * tid + j;
+      c[j] = e < E ? cnt[e] : 0;
+      tl[j] = (c[j] + kGrpBM - 1) / kGrpBM;
+      cs += c[j];
+      ts += tl[j];
+    }
+    int ic = cs, it = ts;  // inclusive scan over the lanes
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int oc = __shfl_up(ic, d, 64), ot = __shfl_up(it, d, 64);
+      if (tid >= d) {
+        ic += oc;
+        it += ot;
+      }
+    }
+    int ec = ic - cs, et = it - ts;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int e = 4 * tid + j;
+      if (e < E) {
+        off[e] = ec;
+        cur[e] = ec;
+        tiles[e] = et;
+      }
+      ec += c[j];
+      et += tl[j];
+    }
+    if (tid == 63) {
+      off[E] = ic;
+      tiles[E] = it;
+    }
+  }
+  __syncthreads();
+  for (int p0 = 0; p0 < n; p0 += P * kSortThreads) {
+    int ev[P];
+    if (n <= P * kSortThreads) {  // one round: the ids of the first pass are still in registers
+#pragma unroll
+      for (int j = 0; j < P; j++) ev[j] = ev0[j];
     } else {
-      inv[p] = -1;
+#pragma unroll
+      for (int j = 0; j < P; j++) {
+        const int p = p0 + j * kSortThreads + tid;
+        ev[j] = p < n ? idx[p] : -1;
+      }
     }
+#pragma unroll
+    for (int j = 0; j < P; j++)
+      if (ev[j] >= 0 && ev[j] < E) perm[atomicAdd(&cur[ev[j]], 1)] = p0 + j * kSortThreads + tid;
   }
 }
 
-// rows[q] = xn[perm[q] / k] for the sorted pairs (16-byte copies); one block per possible row,
-// blocks past the valid count exit.
-__global__ void __launch_bounds__(128) moe_gather_kernel(const f16* __restrict__ xn, int64_t ldx, const int* __restrict__ perm,
-                                                         const int* __restrict__ off, int E, int k, int H,
-                                                         f16* __restrict__ rows) {
-  const int q = blockIdx.x;
-  if (q >= off[E]) return;
-  const u32x4* src = reinterpret_cast<const u32x4*>(xn + (int64_t)(perm[q] / k) * ldx);
-  u32x4* dst = reinterpret_cast<u32x4*>(rows + (int64_t)q * H);
-  for (int i = threadIdx.x; i < H / 8; i += blockDim.x) dst[i] = src[i];
-}
-
-// x[t] += scale * fp16(sum_j w_tj * y[inv[t*k + j]]) with the GEMV path's roundings; one block
-// per token, 8 columns per thread.
-__global__ void __launch_bounds__(128) moe_combine_kernel(const f16* __restrict__ y, const int* __restrict__ inv,
-                                                          const float* __restrict__ wts, int k, int H, int flags,
-                                                          float scale, f16* x, int64_t ldx) {
+// x[t] += scale * fp16(sum_j w_tj * y[t*k + j]) with the GEMV path's roundings, the slots in order
+// (y in pair order, as the grouped down GEMM scatters it; a slot whose expert id lies outside
+// [0, E) has no row and contributes nothing). One block per token, 8 columns per thread; a
+// thread's k rows are requested together.
+template <int KM>
+__global__ void __launch_bounds__(128) moe_combine_kernel(const f16* __restrict__ y, const int* __restrict__ idx,
+                                                          const float* __restrict__ wts, int k, int E, int H,
+                                                          int flags, float scale, f16* x, int64_t ldx) {
   const int t = blockIdx.x;
   f16* xr = x + (int64_t)t * ldx;
+  bool ok[KM];
+  float wj[KM];
+#pragma unroll
+  for (int j = 0; j < KM; j++) {
+    const int e = j < k ? idx[(int64_t)t * k + j] : -1;
+    ok[j] = e >= 0 && e < E;
+    wj[j] = j < k ? wts[(int64_t)t * k + j] : 0.f;
+  }
   for (int i = threadIdx.x; i < H / 8; i += blockDim.x) {
+    // every slot's row is requested at once, a skipped slot's too (its bytes lie inside y and are
+    // never used), so the loads do not wait for the ids
+    f16x8 v[KM];
+#pragma unroll
+    for (int j = 0; j < KM; j++)
+      v[j] = j < k ? *reinterpret_cast<const f16x8*>(y + ((int64_t)t * k + j) * H + 8 * i) : f16x8{};
+    f16x8 xv = *reinterpret_cast<const f16x8*>(xr + 8 * i);
     float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < k; j++) {
-      const int q = inv[(int64_t)t * k + j];
-      if (q < 0) continue;
-      const float w = wts[(int64_t)t * k + j];
-      const f16x8 v = *reinterpret_cast<const f16x8*>(y + (int64_t)q * H + 8 * i);
+#pragma unroll
+    for (int j = 0; j < KM; j++) {
+      if (!ok[j]) continue;  // uniform over the block
 #pragma unroll
       for (int u = 0; u < 8; u++) {
-        float c = (float)v[u] * w;
+        float c = (float)v[j][u] * wj[j];
         asm volatile("" : "+v"(c));  // the fp32 product is what gets rounded to fp16
         s[u] += (flags & kMoeFp16Weights) ? (float)(f16)c : c;
       }
     }
-    f16x8 xv = *reinterpret_cast<const f16x8*>(xr + 8 * i);
 #pragma unroll
     for (int u = 0; u < 8; u++) {
       f16 o = (f16)s[u];
       if (scale != 1.f) {
-        float t = (float)o * scale;
-        asm volatile("" : "+v"(t));  // fp32 product, then fp16 (two roundings)
-        o = (f16)t;
+        float tt = (float)o * scale;
+        asm volatile("" : "+v"(tt));  // fp32 product, then fp16 (two roundings)
+        o = (f16)tt;
       }
       xv[u] = xv[u] + o;
     }
@@ -439,12 +483,13 @@ __global__ void __launch_bounds__(128) moe_combine_kernel(const f16* __restrict_
   }
 }
 
+// One grouped MFMA GEMM launch over the experts (gemm_kernel in grouped mode, tile kGrpBM x kGrpBN):
+// sorted rows [off[e], off[e+1]) of expert e times W + e * wstride_bytes. gather: A row q is
+// A row perm[q] / k (A has a_rows rows); scatter: C row q goes to C row perm[q].
 template <int EPI>
-int grouped_gemm(const f16* A, int lda, const f16* W, int64_t wstride_bytes, f16* C, int ldc, int N, int K,
-                 const int* off, const int* tiles, int E, int max_row_tiles, hipStream_t s) {
-  constexpr int cfg = kGemmGrpCfg;
-  static_assert(kGemmCfgs[cfg].bm == kGrpBM && kGemmCfgs[cfg].bn == kGrpBN && kGemmCfgs[cfg].bk == kGemmBK,
-                "grouped tile");
+int grouped_gemm(const f16* A, int lda, int a_rows, const f16* W, int64_t wstride_bytes, f16* C, int ldc, int N, int K,
+                 const int* off, const int* tiles, const int* perm, int k, bool gather, bool scatter, int E,
+                 int max_row_tiles, hipStream_t s) {
   GemmArgs g{};
   g.A = A;
   g.lda = lda;
@@ -460,9 +505,14 @@ int grouped_gemm(const f16* A, int lda, const f16* W, int64_t wstride_bytes, f16
   g.grp_tiles = tiles;
   g.grp_n = E;
   g.grp_wstride = wstride_bytes;
-  auto fn = gemm_kernel<kGrpBM, kGrpBN, kGemmCfgs[cfg].wm, kGemmCfgs[cfg].wn, kGemmCfgs[cfg].st, EPI, false, true>;
-  const size_t lds = gemm_lds_bytes(cfg, false);
-  constexpr int threads = 64 * kGemmCfgs[cfg].wm * kGemmCfgs[cfg].wn;
+  g.grp_perm = perm;
+  g.grp_k = k;
+  g.grp_a_rows = a_rows;
+  g.grp_gather = gather;
+  g.grp_scatter = scatter;
+  auto fn = gemm_kernel<kGrpBM, kGrpBN, kGrpWM, kGrpWN, kGrpStages, EPI, false, true>;
+  const size_t lds = (size_t)kGrpStages * (kGrpBM + kGrpBN) * kGemmBK * 2;
+  constexpr int threads = 64 * kGrpWM * kGrpWN;
   if (hi_blocks_per_cu(reinterpret_cast<const void*>(fn), threads, lds) <= 0) HI_FAIL("moe: grouped GEMM does not fit");
   const int tiles_n = (N + kGrpBN - 1) / kGrpBN;
   hipLaunchKernelGGL(fn, dim3(max_row_tiles * tiles_n), dim3(threads), lds, s, g);
@@ -476,26 +526,44 @@ size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 int gemv_max() { return hi_gemv_max_rows(); }
 
 // The expert workspace (hi_moe_work_bytes), each piece on a 256-byte boundary. The first
-// kMoeBarBytes (at a fixed offset, whatever M) hold the one-token launch's arrival counters.
+// kMoeBarBytes (at a fixed offset, whatever M) hold the one-token launch's arrival counters and the
+// grouped router's arrival counter; then perm [n], off and tiles [E+1] int, y [n, H] (pair order)
+// and act [n, I] fp16 (sorted order on the grouped path, pair order on the GEMV path).
 constexpr int kMoeBarStride = 64;                 // words between two arrival counters (256 bytes)
 constexpr size_t kMoeBarBytes = 9 * 256;          // 8 counters, then the 8 expected totals
 struct MoeWork {
   unsigned* bar;
-  int *perm, *inv, *off, *tiles;
-  f16 *rows, *y, *act;
+  int *perm, *off, *tiles;
+  f16 *y, *act;
 };
 MoeWork moe_work(void* work, int n, int E, int H) {
   char* p = (char*)work;
   MoeWork m;
   m.bar = (unsigned*)p; p += kMoeBarBytes;
   m.perm = (int*)p;   p += al256((size_t)n * 4);
-  m.inv = (int*)p;    p += al256((size_t)n * 4);
   m.off = (int*)p;    p += al256((size_t)(E + 1) * 4);
   m.tiles = (int*)p;  p += al256((size_t)(E + 1) * 4);
-  m.rows = (f16*)p;   p += al256((size_t)n * H * 2);
   m.y = (f16*)p;      p += al256((size_t)n * H * 2);
   m.act = (f16*)p;
   return m;
+}
+
+// The grouped path after the sort (perm / off / tiles in wk): gate/up + SwiGLU on the rows of xn
+// gathered by the tile DMA (act in sorted order), down scattered to pair order (y), the combine.
+int moe_grouped(const f16* xn, int ldxn, const f16* Wgu, const f16* Wd, const int* idx, const float* w, int M, int E,
+                int k, int H, int I, int flags, float scale, f16* x, int ldx, const MoeWork& wk, hipStream_t st) {
+  const int n = M * k;
+  const int max_row_tiles = (n + kGrpBM - 1) / kGrpBM + E;  // each expert adds at most one partial tile
+  if (int r = grouped_gemm<2>(xn, ldxn, M, Wgu, (int64_t)2 * I * H * 2, wk.act, I, 2 * I, H, wk.off, wk.tiles, wk.perm,
+                              k, true, false, E, max_row_tiles, st))
+    return r;
+  if (int r = grouped_gemm<0>(wk.act, I, n, Wd, (int64_t)H * I * 2, wk.y, H, H, I, wk.off, wk.tiles, wk.perm, 1, false,
+                              true, E, max_row_tiles, st))
+    return r;
+  const auto comb = k <= 4 ? moe_combine_kernel<4> : k <= 8 ? moe_combine_kernel<8> : moe_combine_kernel<16>;
+  hipLaunchKernelGGL(comb, dim3(M), dim3(128), 0, st, wk.y, idx, w, k, E, H, flags, scale, x, (int64_t)ldx);
+  HI_TRY(hipGetLastError());
+  return 0;
 }
 
 // The GEMV path's down projection + weighted combine + residual.
@@ -829,12 +897,12 @@ HI_EXPORT int hi_moe_router(const void* xn, int ldx, const void* Wr, int M, int 
   return 0;
 }
 
-// Expert workspace, each piece on a 256-byte boundary: the one-token launch's arrival counters
-// (2304 bytes, first, whatever M), perm, inv [M*k] int, off, tiles [E+1] int, rows [M*k, H],
-// y [M*k, H] and act [M*k, I] fp16. The GEMV path uses only act.
+// Expert workspace, each piece on a 256-byte boundary: arrival counters (2304 bytes, first,
+// whatever M), perm [M*k] int, off, tiles [E+1] int, y [M*k, H] and act [M*k, I] fp16. The GEMV
+// path uses only act.
 HI_EXPORT size_t hi_moe_work_bytes(int M, int k, int E, int H, int I) {
   const size_t n = (size_t)(M > 0 ? M : 0) * (k > 0 ? k : 0);
-  return kMoeBarBytes + 2 * al256(n * 4) + 2 * al256((size_t)(E + 1) * 4) + 2 * al256(n * H * 2) + al256(n * I * 2);
+  return kMoeBarBytes + al256(n * 4) + 2 * al256((size_t)(E + 1) * 4) + al256(n * H * 2) + al256(n * I * 2);
 }
 
 // x[m] += MoE(xn[m]) for M rows given the routing (idx, w from hi_moe_router): wgu [E][2I, H]
@@ -868,24 +936,9 @@ HI_EXPORT int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const vo
     HI_TRY(hipGetLastError());
     return moe_down_launch(wk.act, Wd, idx, w, M, k, E, H, I, flags, scale, x, ldx, st);
   }
-  int* perm = wk.perm;
-  int* inv = wk.inv;
-  int* off = wk.off;
-  int* tiles = wk.tiles;
-  f16* rows = wk.rows;
-  f16* y = wk.y;
-  f16* act = wk.act;
-  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(1024), 0, st, idx, n, E, off, tiles, perm, inv);
+  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), 0, st, idx, n, E, wk.off, wk.tiles, wk.perm);
   HI_TRY(hipGetLastError());
-  hipLaunchKernelGGL(moe_gather_kernel, dim3(n), dim3(128), 0, st, (const f16*)xn, (int64_t)ldxn, perm, off, E, k, H, rows);
-  HI_TRY(hipGetLastError());
-  const int max_row_tiles = (n + kGrpBM - 1) / kGrpBM + E;  // each expert adds at most one partial tile
-  if (int r = grouped_gemm<2>(rows, H, Wgu, (int64_t)2 * I * H * 2, act, I, 2 * I, H, off, tiles, E, max_row_tiles, st))
-    return r;
-  if (int r = grouped_gemm<0>(act, I, Wd, (int64_t)H * I * 2, y, H, H, I, off, tiles, E, max_row_tiles, st)) return r;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3(M), dim3(128), 0, st, y, inv, w, k, H, flags, scale, (f16*)x, (int64_t)ldx);
-  HI_TRY(hipGetLastError());
-  return 0;
+  return moe_grouped((const f16*)xn, ldxn, Wgu, Wd, idx, w, M, E, k, H, I, flags, scale, (f16*)x, ldx, wk, st);
 }
 
 // Router and experts in one call: x[m] += MoE(xn[m]) for M rows, with the routing computed here and
@@ -904,10 +957,6 @@ HI_EXPORT int hi_moe_route_experts(const void* xn, int ldxn, const void* Wr, con
   if (!d) return -2;
   if (M < 0) HI_FAIL("hi_moe_route_experts: M %d < 0", M);
   if (M == 0) return 0;
-  if (M > gemv_max()) {
-    if (int r = hi_moe_router(xn, ldxn, Wr, M, E, H, k, flags, idx, w, s)) return r;
-    return hi_moe_experts(xn, ldxn, wgu, wdown, idx, w, M, E, k, H, I, flags, scale, x, ldx, 0, work, s);
-  }
   if (E < 1 || E > kMoeMaxE || k < 1 || k > kMoeMaxK || k > E)
     HI_FAIL("hi_moe_route_experts: unsupported E %d / k %d (E <= %d, k <= %d, k <= E)", E, k, kMoeMaxE, kMoeMaxK);
   if (H % 32 || I % 32 || H < 32 || I < 32) HI_FAIL("hi_moe_route_experts: H %d and I %d must be multiples of 32", H, I);
@@ -919,6 +968,13 @@ HI_EXPORT int hi_moe_route_experts(const void* xn, int ldxn, const void* Wr, con
   const hipStream_t st = (hipStream_t)s;
   const int n = M * k;
   const MoeWork wk = moe_work(work, n, E, H);
+  if (M > gemv_max()) {  // the router, then the grouped experts (sort, two GEMMs, combine)
+    if (int r = hi_moe_router(xn, ldxn, Wr, M, E, H, k, flags, idx, w, s)) return r;
+    hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), 0, st, idx, n, E, wk.off, wk.tiles, wk.perm);
+    HI_TRY(hipGetLastError());
+    return moe_grouped((const f16*)xn, ldxn, (const f16*)wgu, (const f16*)wdown, idx, w, M, E, k, H, I, flags, scale,
+                       (f16*)x, ldx, wk, st);
+  }
   if (M == 1) {
     const int r = moe_decode_one(xn, Wr, wgu, wdown, E, k, H, I, flags, scale, x, idx, w, wk.act, wk.bar, st);
     if (r <= 0) return r;  // launched (0) or failed (< 0); 1: this shape takes the two launches

@@ -112,7 +112,9 @@ int hi_moe_experts(const void* xn, int ldxn, const void* wgu, const void* wdown,
  * combine) when that grid fits on the GPU at once; otherwise, for M <= HIPINFER_GEMV_MAX, the router
  * runs inside the gate/up launch. work: hi_moe_work_bytes(M, k, E, H, I), zeroed once before its
  * first use with this function (the one-launch path keeps arrival counters in it and leaves them
- * consistent); calls that share a work buffer must not overlap in time.
+ * consistent); calls that share a work buffer must not overlap in time. Returns -2, launching
+ * nothing, when an earlier one-launch call gave up waiting for its grid (its output was wrong; the
+ * one-launch path is then off for the rest of the process).
  * No counterpart in the reference (its engine makes the two calls, api.cu:1701-1703); for callers
  * that run a whole MoE layer, such as this library's engine. */
 int hi_moe_route_experts(const void* xn, int ldxn, const void* Wr, const void* wgu, const void* wdown, int M, int E,

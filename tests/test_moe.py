@@ -146,7 +146,7 @@ def test_moe_route_experts_is_router_then_experts(hi, name, E, k, H, I, flags, s
     r = rng(440 + E)
     Wr = cuda(rn(r, E, H, s=0.05))
     wgu, wdn = cuda(rn(r, E, 2 * I, H, s=0.02)), cuda(rn(r, E, H, I, s=0.02))
-    for M in [1, 2, 3, 4, 5, 37]:
+    for M in [1, 2, 3, 4, 5, 37, 300]:
         xn, x0 = cuda(rn(r, M, H)), cuda(rn(r, M, H))
         idx2, w2 = hi.moe_router(xn, Wr, k, flags)
         ref = host(hi.moe_experts(xn, wgu, wdn, idx2, w2, x0.clone(), flags, scale, 0))
@@ -189,6 +189,46 @@ def test_moe_route_experts_graph_replay(hi):
         assert np.array_equal(host(x).view(np.uint16), ref.view(np.uint16))
         assert np.array_equal(host(idx), host(idx2))
         hi.moe_route_experts(xn, Wr, wgu, wdn, k, x0.clone(), flags, 0.22)  # eager work between replays
+
+
+def test_moe_route_experts_grouped_graph_replay(hi):
+    """Above the GEMV row limit (router, sort, two grouped GEMMs with gathered A rows and scattered
+    C rows, combine): captured in a graph and replayed, with eager calls on the same work buffer
+    between replays, every result equals the router + grouped experts bit for bit."""
+    import torch
+    r = rng(455)
+    E, k, H, I, flags, M = 32, 8, 1024, 512, 3, 256
+    Wr, wgu, wdn = cuda(rn(r, E, H, s=0.05)), cuda(rn(r, E, 2 * I, H, s=0.02)), cuda(rn(r, E, H, I, s=0.02))
+    xn, x0 = cuda(rn(r, M, H)), cuda(rn(r, M, H))
+    idx2, w2 = hi.moe_router(xn, Wr, k, flags)
+    ref = host(hi.moe_experts(xn, wgu, wdn, idx2, w2, x0.clone(), flags, 0.22, 2))
+    x = x0.clone()
+    idx = torch.empty(M, k, dtype=torch.int32, device="cuda")
+    w = torch.empty(M, k, dtype=torch.float32, device="cuda")
+    work = torch.zeros(hi.lib.hi_moe_work_bytes(M, k, E, H, I), dtype=torch.uint8, device="cuda")
+
+    def run(xx):
+        hi.check_rc(hi.lib.hi_moe_route_experts(hi.ptr(xn), H, hi.ptr(Wr), hi.ptr(wgu), hi.ptr(wdn), M, E, k, H, I, flags,
+                                                0.22, hi.ptr(xx), H, hi.ptr(idx), hi.ptr(w), hi.ptr(work),
+                                                hi.cur_stream()), "moe_route_experts")
+    run(x)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(x).view(np.uint16), ref.view(np.uint16))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run(x)
+    for _ in range(3):
+        x.copy_(x0)
+        idx.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(x).view(np.uint16), ref.view(np.uint16))
+        assert np.array_equal(host(idx), host(idx2))
+        xe = x0.clone()
+        run(xe)  # eager work on the same buffer between replays
+        torch.cuda.synchronize()
+        assert np.array_equal(host(xe).view(np.uint16), ref.view(np.uint16))
 
 
 def test_moe_route_experts_shared_work_across_shapes(hi):
