@@ -338,6 +338,16 @@ def prefill_bench(torch, hi, steps, warmup, q8_too):
                                             "pct_hbm_ceiling": round(100 * hbm_us / us, 1)}
             del g
         b = pm.buffers(1024)
+        # gate/up inside the layer: the layer pass minus the same pass without its gate/up launches
+        # (the kernel alone, back to back, runs slower: see the roofline_mfma note)
+        g = capture(torch, lambda: pm.layer_pass(b, q8, kinds=("qkv", "o", "down")))
+        ms, _ = time_graph(torch, g, max(3, steps // 2), warmup)
+        del g
+        gu_in = res["layers"][f"M1024_{tag}"]["us_per_layer"] - ms * 1e3 / P_L
+        N, K = P_SHAPES["gate_up"]
+        res["gate_up_in_layer_m1024_" + tag] = {
+            "us": round(gu_in, 2), "TFLOP/s": round(2.0 * 1024 * N * K / (gu_in * 1e-6) / 1e12, 1),
+            "how": "M = 1024 layer pass minus the same pass without the gate/up launches (HIP events, median replays)"}
         for kind in P_SHAPES:
             g = capture(torch, lambda: pm.layer_pass(b, q8, kinds=(kind,)))
             ms, _ = time_graph(torch, g, max(3, steps // 2), warmup)
@@ -848,6 +858,42 @@ def gemm_counters(csv_paths, cus=256, xcds=8, replays=3):
             print(f"| {k} | " + " | ".join(row) + " |")
 
 
+def gemm_clock(trace_csv, counter_csv, replays, xcds=8):
+    """Shader clock of the M = 1024 gate/up GEMM inside the layer and back to back, from two runs of
+    `bench.py --profile gemm_clock --steps <replays>`: a rocprofv3 --kernel-trace run (durations) and a
+    --pmc GRBM_GUI_ACTIVE run (GPU-active cycles, the raw counter summed over the XCDs' copies). The
+    profile ends with `replays` layer passes (28 x QKV, o, gate/up, down) and then `replays` passes of
+    the 28 gate/up launches alone (each preceded by one eager pass); the gate/up launch is every
+    fourth GEMM of a layer pass. Prints duration, cycles and cycles per microsecond (MHz) per mode."""
+    import csv
+    trace = []
+    with open(trace_csv) as f:
+        for r in csv.DictReader(f):
+            if "gemm_kernel" in r["Kernel_Name"]:
+                trace.append((int(r["Dispatch_Id"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    trace.sort()
+    cyc, cdur = {}, {}
+    with open(counter_csv) as f:
+        for r in csv.DictReader(f):
+            if "gemm_kernel" in r["Kernel_Name"] and r["Counter_Name"] == "GRBM_GUI_ACTIVE":
+                k = int(r["Dispatch_Id"])
+                cyc[k] = cyc.get(k, 0.0) + float(r["Counter_Value"])
+                cdur[k] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    cycles = [cyc[k] / xcds for k in sorted(cyc)]
+    cdurs = [cdur[k] for k in sorted(cyc)]
+    n_gu, n_layer = replays * P_L, replays * P_L * 4
+    durs = [d for _, d in trace]
+    lay = slice(-n_gu - P_L - n_layer, -n_gu - P_L)
+    modes = {"back to back (28 gate/up launches per pass)": (durs[-n_gu:], cycles[-n_gu:], cdurs[-n_gu:]),
+             "inside the layer pass (every 4th GEMM)": (durs[lay][2::4], cycles[lay][2::4], cdurs[lay][2::4])}
+    print("| gate/up (M = 1024) | launches | mean us (trace run) | mean us (counter run) | GPU-active cycles per "
+          "launch (per XCD) | cycles per us of the counter run |")
+    print("|---|---|---|---|---|---|")
+    for name, (d, c, cd) in modes.items():
+        md, mc, mcd = sum(d) / len(d), sum(c) / len(c), sum(cd) / len(cd)
+        print(f"| {name} | {len(d)} | {md:.2f} | {mcd:.2f} | {mc:.0f} | {mc / mcd:.0f} |")
+
+
 def gemv_counters(csv_paths, layers=28):
     """Per-kind counters of `bench.py --profile c4` (the C4 GEMV set at 8 rows, fp16 tokens then int8
     tokens), from one or more rocprofv3 `--pmc` counter CSVs of the same command (one counter pass
@@ -902,6 +948,9 @@ def main():
     if len(sys.argv) == 3 and sys.argv[1] == "--timeline":
         timeline(sys.argv[2])
         return
+    if len(sys.argv) == 5 and sys.argv[1] == "--gemm-clock":
+        gemm_clock(sys.argv[2], sys.argv[3], int(sys.argv[4]))
+        return
     if len(sys.argv) >= 3 and sys.argv[1] == "--gemm-counters":
         gemm_counters(sys.argv[2:])
         return
@@ -921,7 +970,8 @@ def main():
     ap.add_argument("--prefill-breakdown", metavar="CSV", default=None,
                     help="(alone) print the per-kernel table of the last prefill (or decode step) in a kernel "
                          "trace of --profile prefill (or decode64)")
-    ap.add_argument("--profile", choices=["token", "token8", "gemm", "moe", "c4", "prefill", "flash", "decode64"] +
+    ap.add_argument("--profile", choices=["token", "token8", "gemm", "gemm_clock", "moe", "c4", "prefill", "flash",
+                                          "decode64"] +
                     [k + q for k in ("qkv", "o", "gate_up", "down", "lm_head") for q in ("", "8")], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
     args = ap.parse_args()
@@ -996,6 +1046,19 @@ def main():
     log(f"weights ready in {time.perf_counter() - t0:.1f} s")
 
     if args.profile:
+        if args.profile == "gemm_clock":
+            # the M = 1024 layer pass, then the gate/up launches alone back to back: `steps` replays of
+            # each, for the shader-clock comparison (--gemm-clock)
+            pm = PrefillModel(torch, hi, False)
+            b = pm.buffers(1024)
+            for kinds in [("qkv", "o", "gate_up", "down"), ("gate_up",)]:
+                g = capture(torch, lambda: pm.layer_pass(b, False, kinds=kinds))
+                for _ in range(args.steps):
+                    g.replay()
+                torch.cuda.synchronize()
+                del g
+            log(f"profile run done (gemm_clock): {args.steps} layer passes, then {args.steps} gate/up passes")
+            return
         if args.profile == "gemm":
             pm = PrefillModel(torch, hi, False)
             b = pm.buffers(1024)
@@ -1086,13 +1149,18 @@ def main():
         log("prefill GEMM ...")
         res["prefill_gemm"] = prefill_bench(torch, hi, args.steps, args.warmup, not args.no_int8)
         gk = res["prefill_gemm"]["kernels_m1024"]["gate_up_fp16"]
+        gi = res["prefill_gemm"]["gate_up_in_layer_m1024_fp16"]
         flops = 2.0 * 1024 * gk["N"] * gk["K"]
         res["roofline_mfma"] = {
             "bound": "mfma", "achieved": gk["TFLOP/s"], "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(gk["TFLOP/s"] / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
             "kernel": "gemm_kernel (tuned tile) gate/up + SwiGLU, Llama-3.2-3B, M=1024, N=16384, K=3072, fp16",
             "launch_flops": flops, "avg_us": gk["us"],
-            "counters": "profiles/gemm_prefill_llama32_3b.md (rocprofv3 MfmaUtil per GEMM kind)"}
+            "avg_us_how": "28 distinct gate/up launches back to back in a graph (HIP events, median replay / 28)",
+            "in_layer_us": gi["us"], "in_layer_frac": round(gi["TFLOP/s"] / MFMA_F16_PEAK_TFLOPS, 4),
+            "in_layer_how": gi["how"],
+            "counters": "profiles/gemm_prefill_llama32_3b.md (rocprofv3 MfmaUtil per GEMM kind; shader clock of the "
+                        "gate/up launches back to back and inside the layer)"}
     if not args.no_configs:
         del g16
         if "int8" in out:
