@@ -357,6 +357,33 @@ def prefill_bench(torch, hi, steps, warmup, q8_too):
             res["kernels_m1024"][f"{kind}_{tag}"] = {"N": N, "K": K, "us": round(us, 2), "TFLOP/s": round(tf, 1),
                                                      "pct_mfma_peak": round(100 * tf / MFMA_F16_PEAK_TFLOPS, 1)}
             del g
+    # for scale: the vendor library (torch.matmul, hipBLASLt / rocBLAS) on the same weights at M = 1024,
+    # plain GEMMs without the fused epilogues, each kind over the 28 layers in a graph
+    try:
+        lib = str(torch.backends.cuda.preferred_blas_library())
+    except Exception:
+        lib = "default"
+    b = pm.buffers(1024)
+    vend = {"library": "torch.matmul (" + lib + ")", "kernels_m1024": {}}
+    tot = 0.0
+    for kind, (N, K) in P_SHAPES.items():
+        A = torch.randn(1024, K, device="cuda").half()
+        outs = torch.empty(1024, N, dtype=torch.float16, device="cuda")
+
+        def run(kind=kind, A=A, outs=outs):
+            for l in range(P_L):
+                torch.matmul(A, pm.layers[l][kind].t(), out=outs)
+        g = capture(torch, run)
+        ms, _ = time_graph(torch, g, max(3, steps // 2), warmup)
+        del g
+        us = ms * 1e3 / P_L
+        tot += us
+        tf = 2.0 * 1024 * N * K / (us * 1e-6) / 1e12
+        vend["kernels_m1024"][kind] = {"us": round(us, 2), "TFLOP/s": round(tf, 1),
+                                       "pct_mfma_peak": round(100 * tf / MFMA_F16_PEAK_TFLOPS, 1)}
+    vend["us_per_layer_sum"] = round(tot, 2)
+    vend["pct_mfma_peak"] = round(100 * flops_layer(1024) / (tot * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 1)
+    res["vendor_m1024_fp16"] = vend
     del pm
     torch.cuda.empty_cache()
     return res

@@ -553,6 +553,9 @@ MoeWork moe_work(void* work, int n, int E, int H) {
 int moe_grouped(const f16* xn, int ldxn, const f16* Wgu, const f16* Wd, const int* idx, const float* w, int M, int E,
                 int k, int H, int I, int flags, float scale, f16* x, int ldx, const MoeWork& wk, hipStream_t st) {
   const int n = M * k;
+  // the tile DMA addresses xn's gathered rows, and act's and y's rows, at 32-bit byte offsets
+  if ((int64_t)M * ldxn * 2 >= INT32_MAX || (int64_t)n * (H > I ? H : I) * 2 >= INT32_MAX)
+    HI_FAIL("moe: %d rows too many for the grouped path's 32-bit offsets", M);
   const int max_row_tiles = (n + kGrpBM - 1) / kGrpBM + E;  // each expert adds at most one partial tile
   if (int r = grouped_gemm<2>(xn, ldxn, M, Wgu, (int64_t)2 * I * H * 2, wk.act, I, 2 * I, H, wk.off, wk.tiles, wk.perm,
                               k, true, false, E, max_row_tiles, st))
