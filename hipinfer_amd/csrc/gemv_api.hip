@@ -33,6 +33,12 @@ int gemv_rows_per_launch(int K, bool norm, bool int8) {
   return d ? rows_per_launch(gemv_row_lds(K, int8), norm, d->lds_max) : 0;
 }
 
+HI_EXPORT int hi_gemv_rows_per_launch(int K, int norm, int int8) {
+  const HiDevice* d = hi_device();
+  if (!d) return -2;
+  return K < 8 ? 0 : rows_per_launch(gemv_row_lds(K, int8 != 0), norm != 0, d->lds_max);
+}
+
 static int gemv_common(GemvArgs a, int epi, hipStream_t s, const char* who) {
   const HiDevice* d = hi_device();
   if (!d) return -2;

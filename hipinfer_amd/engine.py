@@ -125,16 +125,12 @@ class DecodeStep:
         GEMV."""
         if B < 2:
             return 0
-        lds = hi.lib.hi_max_smem()
         mask = 0
         dq8 = isinstance(weights["layers"][0]["down"], tuple)
-        # LDS per activation row of a GEMV launch (8 waves of 64): the row, 9 floats of norm
-        # partials and inverse RMS, and with int8 weights one float per staging thread
-        row = cfg["I"] * 2 + 9 * 4 + (512 * 4 if dq8 else 0)
-        fit = 16
-        while fit > 1 and fit * row > lds:
-            fit //= 2
-        if row > lds or B > fit or (dq8 and B >= 5):
+        fit = hi.lib.hi_gemv_rows_per_launch(cfg["I"], 0, int(dq8))
+        if fit < 0:
+            raise RuntimeError(f"hi_gemv_rows_per_launch failed ({fit})")
+        if B > fit or (dq8 and B >= 5):
             mask |= DOWN_GEMM
         if isinstance(weights["lm"], tuple) and B >= 5:
             mask |= LM_GEMM

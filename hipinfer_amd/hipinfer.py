@@ -51,6 +51,7 @@ int hi_quantize_rows(ptr w, i64 N, int K, ptr q, ptr s, ptr stream);
 int hi_dequantize_rows(ptr q, ptr s, i64 N, int K, ptr out, ptr stream);
 int hi_device_cus();
 int hi_max_smem();
+int hi_gemv_rows_per_launch(int K, int norm, int int8);
 int hi_gemm(ptr A, int lda, ptr W, ptr bias, ptr C, int ldc, int M, int N, int K, int epi, ptr stream);
 int hi_gemm_w8(ptr A, int lda, ptr W, ptr scales, ptr bias, ptr C, int ldc, int M, int N, int K, int epi, ptr stream);
 int hi_gemm_force_config(int cfg);

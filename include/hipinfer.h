@@ -175,6 +175,11 @@ int hi_device_cus(void);
 /* Largest dynamic LDS (bytes) a block may opt into on the current device: 160 KB on MI355X.
  * Replaces api.cu:49 (hi_max_smem, the CUDA shared-memory opt-in). */
 int hi_max_smem(void);
+/* Activation rows one GEMV launch takes at K (norm: fused RMSNorm, int8: int8 weights) on the
+ * current device; more rows run in row chunks, each streaming the weights again. 0 when one row does
+ * not fit, -2 on a HIP error. No counterpart in the reference; for hosts choosing between the GEMV and
+ * the GEMM for small batches, such as hipinfer_amd.engine.DecodeStep. */
+int hi_gemv_rows_per_launch(int K, int norm, int int8);
 
 /* ---- engine: weight-file loader, prefill, graph-captured greedy decode (one GPU)
  * An opaque engine over a weight file in the reference's export format (scripts/export.py:5-38;

@@ -250,6 +250,17 @@ def test_max_smem_bounds_the_activation_rows(hi, O):
         hi.gemv(torch.zeros(1, K, dtype=torch.float16, device="cuda"), torch.zeros(16, K, dtype=torch.float16, device="cuda"))
 
 
+def test_rows_per_launch(hi):
+    """hi_gemv_rows_per_launch: 8 rows with the fused norm and 16 without while they fit the LDS,
+    halved until they do (the Llama-3.1-8B down projection's 28 KB rows: 4), 0 for a row longer
+    than the LDS; the launcher's row chunks follow it (checked above at M = 16, K = 14336)."""
+    lim = hi.lib.hi_max_smem()
+    f = hi.lib.hi_gemv_rows_per_launch
+    assert f(4096, 1, 0) == 8 and f(4096, 0, 0) == 16 and f(1536, 0, 1) == 16
+    assert f(14336, 0, 0) == 4 and f(14336, 0, 1) == 4
+    assert f((lim // 2 // 8 + 8) * 8, 0, 0) == 0
+
+
 def test_rejects_bad_arguments(hi):
     import torch
     x = torch.zeros(1, 12, dtype=torch.float16, device="cuda")
