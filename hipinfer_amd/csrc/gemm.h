@@ -663,8 +663,9 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(const float* __restric
 // (eight waves: two 4-wave pipelines on the two halves of the K tiles, each with its own 2-stage
 // ring, group 1's sums handed to group 0 through LDS at the end), puts two waves on each SIMD
 // for the same one-tile-per-CU cut of N = 5120: QKV of Llama-3.2-3B at M = 1024 in 42.3 against
-// 45.6 us. The same split of 128 x 96 (o, down) measured no faster: those tiles are bound by the
-// LDS reads of the W rows every wave re-reads, not by latency.
+// 45.6 us. The same split of 128 x 96 (o, down) measured no faster, and neither did four-wave
+// tiles whose waves hold 64 rows (37 % fewer LDS fragment reads per MFMA): neither latency nor the
+// LDS reads bound the narrow tiles.
 struct GemmCfg {
   int bm, bn, wm, wn, st, bk, kg = 1;  // kg: K groups of wm x wn waves (two waves on each SIMD at kg 2)
 };
