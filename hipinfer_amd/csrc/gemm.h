@@ -693,7 +693,7 @@ constexpr bool gemm_cfg_fits(int c, bool q8, int K) {
 // per CU). 128 rows hold a whole expert's share of a 256-token prefill (top-8 of 32 experts: about
 // 64 rows each), so each expert's weights are streamed once; a 64-row tile split most experts into
 // two row tiles, each streaming the same weights.
-constexpr int kGrpBM = 128, kGrpBN = 128, kGrpWM = 2, kGrpWN = 2, kGrpStages = 4;  // 64-deep K tiles
+constexpr int kGrpBM = 128, kGrpBN = 128, kGrpWM = 2, kGrpWN = 2, kGrpStages = 4, kGrpBK = 64;
 inline size_t gemm_lds_bytes(int cfg, bool q8) {
   const GemmCfg& c = kGemmCfgs[cfg];
   return (size_t)c.kg * c.st * (c.bm * c.bk * 2 + c.bn * (q8 ? c.bk : 2 * c.bk));
