@@ -57,6 +57,7 @@ struct GemmArgs {
   int kt_per_split;    // K tiles per split (gridDim.y splits)
   float* ws;           // split-K partials: [splits][M][N] fp32
   bool vec_c;          // C (and the residual read) allow 8-byte accesses: C 8-byte aligned, ldc % 4 == 0
+  bool vec16_c;        // ... and 16-byte ones (C 16-byte aligned, ldc % 8 == 0): the LDS-staged epilogue
   // grouped mode (MoE experts): group e owns sorted rows [grp_off[e], grp_off[e+1]) and the
   // weights at W + e * grp_wstride bytes; its row tiles are [grp_tiles[e], grp_tiles[e+1]) of the
   // global row-tile count (block id / column tiles). Sorted row q is A row q and C row q, unless
@@ -549,6 +550,78 @@ __global__ void __launch_bounds__(64 * WM * WN * KG) gemm_kernel(GemmArgs g) {
   // ---- result layout (W fragment as the MFMA's first operand): lane (fk, fr) of tile (i, j) holds
   //      row fr of the tile's 32 rows, columns 8 g + 4 fk + 0..3 in acc[i][j][4 g .. 4 g + 3]:
   //      four consecutive output columns per register quad
+
+  // ---- staged epilogue (grouped tiles and the one-wave-wide 128 x 96 / 128 x 160 tiles; one K
+  //      group, no split, C 16-byte addressable): the finished fp16 tile goes through LDS and leaves
+  //      in 16-byte chunks, whole row segments per store instruction. Stored straight from the
+  //      fragments, each store instruction writes 16 bytes into each of 32 rows (about 150 ns per
+  //      instruction measured on the grouped down GEMM, 16 per lane there, 12-20 on the wide-wave
+  //      tiles); staged, four to six rows of contiguous chunks. Other tiles keep the direct path:
+  //      there the staged code cost registers (4-12 VGPRs, more spills on 256 x 256) for no gain.
+  //      The roundings are the direct path's: the bias is added in fp32 before the fp16 rounding,
+  //      SwiGLU is formed from the fp32 sums, and the residual is added (fp16 add) to the rounded
+  //      product in the copy.
+  constexpr bool kStaged = KG == 1 && (GRP || WN == 1);
+  if (kStaged && gridDim.y == 1 && g.vec16_c) {
+    constexpr int BNO = EPI == 2 ? BN / 2 : BN;  // output columns of the tile
+    // LDS row stride in halves: 16 bytes of padding put the 32 rows one fragment write covers on
+    // every bank once per 16 rows (BNO % 16 == 0)
+    constexpr int CS = BNO + 8;
+    static_assert(BNO % 16 == 0, "staged tile row padding");
+    f16* cs = reinterpret_cast<f16*>(smem_raw);
+    int* s_row = reinterpret_cast<int*>(cs + BM * CS);  // C row of each tile row
+    barrier_no_fence();  // every wave is done with the rings (their DMA landed above)
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      const int lr = wm * TM + i * 32 + fr;
+      if (wn == 0 && fk == 0) s_row[lr] = c_row[i];
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        const int lc0 = wn * TN + j * 32;  // the 32-column MFMA tile's first column in the tile
+        if constexpr (EPI == 2) {
+#pragma unroll
+          for (int q = 0; q < 2; q++) {
+            f16x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = silu_mul_fast(acc[i][j][4 * q + e], acc[i][j][4 * q + 8 + e]);
+            *reinterpret_cast<f16x4*>(cs + lr * CS + (lc0 >> 1) + 8 * q + 4 * fk) = o;
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const int lc = lc0 + 8 * q + 4 * fk;
+            f16x4 o;
+            if constexpr (EPI == 1) {
+#pragma unroll
+              for (int e = 0; e < 4; e++) o[e] = (f16)acc[i][j][4 * q + e];
+            } else {
+              f16x4 b = {(f16)0.f, (f16)0.f, (f16)0.f, (f16)0.f};
+              if (g.bias && bn + lc < N) b = load4(g.bias + bn + lc, ((uintptr_t)g.bias & 7) == 0);
+#pragma unroll
+              for (int e = 0; e < 4; e++) o[e] = (f16)(acc[i][j][4 * q + e] + (float)b[e]);
+            }
+            *reinterpret_cast<f16x4*>(cs + lr * CS + lc) = o;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    constexpr int CPR = BNO / 8;  // 16-byte chunks per tile row
+    const int bno = EPI == 2 ? bn / 2 : bn, ncol = min((EPI == 2 ? N / 2 : N) - bno, BNO);
+    for (int c = tid; c < BM * CPR; c += 64 * NW) {
+      const int r = c / CPR, cc = c - r * CPR;
+      if (r >= valid_m || cc * 8 >= ncol) continue;  // N % 16 == 0: a chunk is all in or all out
+      f16x8 v = *reinterpret_cast<const f16x8*>(cs + r * CS + cc * 8);
+      f16* dst = Cp + (int64_t)s_row[r] * g.ldc + bno + cc * 8;
+      if constexpr (EPI == 1) {
+        const f16x8 rv = *reinterpret_cast<const f16x8*>(dst);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = rv[e] + v[e];  // fp16 add, correctly rounded
+      }
+      *reinterpret_cast<f16x8*>(dst) = v;
+    }
+    return;
+  }
   if (gridDim.y > 1) {
     // split-K: this split's fp32 partial [split][M][N]; a second kernel (gemm_splitk_reduce) sums
     // the splits in order and runs the epilogue, after the kernel boundary made them visible
@@ -694,9 +767,13 @@ constexpr bool gemm_cfg_fits(int c, bool q8, int K) {
 // 64 rows each), so each expert's weights are streamed once; a 64-row tile split most experts into
 // two row tiles, each streaming the same weights.
 constexpr int kGrpBM = 128, kGrpBN = 128, kGrpWM = 2, kGrpWN = 2, kGrpStages = 4, kGrpBK = 64;
+// LDS of the staged epilogue: the fp16 tile with 16-byte row padding, then one C row index per row
+constexpr size_t gemm_stage_bytes(int bm, int bn) { return (size_t)bm * (bn + 8) * 2 + (size_t)bm * 4; }
 inline size_t gemm_lds_bytes(int cfg, bool q8) {
   const GemmCfg& c = kGemmCfgs[cfg];
-  return (size_t)c.kg * c.st * (c.bm * c.bk * 2 + c.bn * (q8 ? c.bk : 2 * c.bk));
+  const size_t ring = (size_t)c.kg * c.st * (c.bm * c.bk * 2 + c.bn * (q8 ? c.bk : 2 * c.bk));
+  const bool staged = c.kg == 1 && c.wn == 1;  // the kernel's kStaged (grouped tiles size their own)
+  return staged && gemm_stage_bytes(c.bm, c.bn) > ring ? gemm_stage_bytes(c.bm, c.bn) : ring;
 }
 
 // Split-K second pass of a residual GEMM fused with the RMSNorm that reads its result: one block

@@ -321,6 +321,7 @@ int gemm_args(const void* A, int lda, const void* W, const void* scales, const v
   g.N = N;
   g.K = K;
   g.vec_c = aligned(C, 8) && ldc % 4 == 0;
+  g.vec16_c = aligned(C, 16) && ldc % 8 == 0;
   return 0;
 }
 

@@ -501,6 +501,7 @@ int grouped_gemm(const f16* A, int lda, int a_rows, const f16* W, int64_t wstrid
   g.K = K;
   g.kt_per_split = (K + kGrpBK - 1) / kGrpBK;
   g.vec_c = true;  // act / y live in the 256-byte aligned work buffer, ldc = I or H (multiples of 32)
+  g.vec16_c = true;
   g.grp_off = off;
   g.grp_tiles = tiles;
   g.grp_n = E;
@@ -511,7 +512,7 @@ int grouped_gemm(const f16* A, int lda, int a_rows, const f16* W, int64_t wstrid
   g.grp_gather = gather;
   g.grp_scatter = scatter;
   auto fn = gemm_kernel<kGrpBM, kGrpBN, kGrpWM, kGrpWN, kGrpStages, EPI, false, true, kGrpBK>;
-  const size_t lds = (size_t)kGrpStages * (kGrpBM + kGrpBN) * kGrpBK * 2;
+  const size_t lds = std::max((size_t)kGrpStages * (kGrpBM + kGrpBN) * kGrpBK * 2, gemm_stage_bytes(kGrpBM, kGrpBN));
   constexpr int threads = 64 * kGrpWM * kGrpWN;
   if (hi_blocks_per_cu(reinterpret_cast<const void*>(fn), threads, lds) <= 0) HI_FAIL("moe: grouped GEMM does not fit");
   const int tiles_n = (N + kGrpBN - 1) / kGrpBN;
