@@ -185,6 +185,62 @@ def test_gemm_writes_nothing_past_n(hi, O, cfg):
         hi.lib.hi_gemm_force_splits(-1)
 
 
+def wide_wave_cfgs(hi):
+    """Configs whose waves each span the tile's full width (waves WM x 1, one K group): the tiles
+    whose epilogue goes through LDS when C rows are 16-byte addressable."""
+    import ctypes
+    import re
+    out = []
+    for cfg in range(hi.lib.hi_gemm_num_configs()):
+        buf = ctypes.create_string_buffer(128)
+        hi.lib.hi_gemm_config_desc(cfg, buf, 128)
+        m = re.search(r"waves (\d+)x(\d+)x(\d+)", buf.value.decode())
+        if int(m[2]) == 1 and int(m[3]) == 1:
+            out.append(cfg)
+    return out
+
+
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_gemm_staged_epilogue_matches_direct(hi, O, epi):
+    """The staged epilogue (C rows 16-byte addressable) and the direct one (ldc % 8 == 4: 8-byte
+    stores only) give the same bits on the tiles that have both, with a partial row tile (M = 200),
+    a last column tile that ends 16 columns past N (N % 32 == 16; SwiGLU N % 32 == 0), a bias, and
+    the residual; the row padding is left alone by both."""
+    import torch
+    cfgs = wide_wave_cfgs(hi)
+    assert cfgs, "no wide-wave tile config"
+    r = rng(390 + epi)
+    M, K = 200, 1024
+    N = 1056 if epi == 2 else 1040
+    n_out = N // 2 if epi == 2 else N
+    A = h16(r, M, K)
+    W = interleave(h16(r, N // 2, K, sd=0.02), h16(r, N // 2, K, sd=0.02)) if epi == 2 else h16(r, N, K, sd=0.02)
+    b = h16(r, N) if epi == 0 else None
+    res = h16(r, M, n_out)
+    ref = O.gemm(A, W, epi=epi, bias=b, out=res.copy() if epi == 1 else None)
+    for cfg in cfgs:
+        hi.lib.hi_gemm_force_config(cfg)
+        hi.lib.hi_gemm_force_splits(1)
+        try:
+            outs = []
+            for pad in (0, 4):  # ldc = n_out (staged), n_out + 4 (direct)
+                buf = np.full((M, n_out + pad), 7.0, np.float16)
+                if epi == 1:
+                    buf[:, :n_out] = res
+                bd = cuda(buf)
+                hi.gemm(cuda(A), cuda(W), out=bd[:, :n_out], epi=epi, bias=None if b is None else cuda(b))
+                got = host(bd)
+                assert last_choice(hi)[0] == cfg
+                assert (got[:, n_out:] == 7.0).all(), f"cfg={cfg} pad={pad}: wrote into the row padding"
+                check(f"cfg={cfg} epi={epi} ldc={n_out + pad}", got[:, :n_out], ref, 4e-3, 4e-3)
+                outs.append(got[:, :n_out])
+            assert np.array_equal(bits(outs[0]), bits(outs[1])), f"cfg={cfg} epi={epi}: staged and direct differ"
+        finally:
+            hi.lib.hi_gemm_force_config(-1)
+            hi.lib.hi_gemm_force_splits(-1)
+            torch.cuda.synchronize()
+
+
 def test_gemm_large_prefill_shapes(hi, O):
     """Llama-3.2-3B prefill shapes at M = 2000 (non-tile-multiple), automatic choice."""
     r = rng(310)
