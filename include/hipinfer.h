@@ -2,7 +2,7 @@
  *
  * Drop-in for the kernel launchers of the reference's src/api.cu that scripts/hipinfer.py binds
  * over ctypes (argtypes at scripts/hipinfer.py:12-31, 66-71). Same symbol names, argument order
- * and meaning. Conventions (reference api.cu:18, SURVEYed in hipinfer.py:101-161):
+ * and meaning. Conventions (reference api.cu:18, as scripts/hipinfer.py:101-161 uses them):
  *   - every tensor is a caller-owned device pointer; leading dimensions are in elements;
  *   - fp16 data is IEEE binary16; int8 weights [N, K] carry one fp16 scale per output row
  *     (W[n, k] ~ q[n, k] * s[n], docs/quantization.md);

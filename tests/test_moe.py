@@ -75,8 +75,9 @@ def test_moe_router_exact_tie(hi):
 
 
 def test_moe_grouped_path_graph_replay(hi, O):
-    """The grouped path launches sort, gather, two grouped GEMMs and the combine with no host
-    round trip, so it can be captured; every replay is checked, with eager work between."""
+    """The grouped path launches the sort, two grouped GEMMs (the first gathering its rows through
+    the tile DMA) and the combine with no host round trip, so it can be captured; every replay is
+    checked, with eager work between."""
     import torch
     r = rng(420)
     E, k, H, I, flags = 32, 8, 1024, 512, 3
