@@ -254,8 +254,13 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
           }
     }
     if constexpr (MR >= 4) {  // one scattered reduction: lane m ends with row m's sum
-      wave_sum_scatter<MR>(ss, lane);
-      if (lane < MR) red[wave][lane] = ss[0];
+      // (padded with zero sums to a power of 2: each sum keeps wave_sum's tree, so its bits)
+      constexpr int MP = pow2_at_least(MR);
+      float sp[MP];
+#pragma unroll
+      for (int m = 0; m < MP; m++) sp[m] = m < MR ? ss[m] : 0.f;
+      wave_sum_scatter<MP>(sp, lane);
+      if (lane < MR) red[wave][lane] = sp[0];
     } else {
 #pragma unroll
       for (int m = 0; m < MR; m++) ss[m] = wave_sum(ss[m]);
@@ -442,22 +447,35 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs a) {
     const bool last = s == SPI - 1;
     if (last) {
       // the R x MR sums over the wave (wave_sum's tree), then each lane's row: from 4 sums on, one
-      // scattered reduction of all of them (accumulator j * MR + m ends in lanes l with
-      // l % L == (j * MR + m) % L, slot (j * MR) / L) and a lane read per sum the epilogue needs
-      constexpr int NA = R * MR, L = NA < 16 ? NA : 16;
+      // scattered reduction of all of them, padded with zero sums to NP, a power of 2 (accumulator
+      // j * MR + m ends in lanes l with l % L == (j * MR + m) % L, slot (j * MR) / L) and a lane read
+      // per sum the epilogue needs
+      constexpr int NA = R * MR, NP = pow2_at_least(NA), L = NP < 16 ? NP : 16;
       float av0[G], av1[G];
       if constexpr (NA >= 4) {
-        float v[NA];
+        float v[NP];
 #pragma unroll
         for (int j = 0; j < R; j++)
 #pragma unroll
           for (int m = 0; m < MR; m++) v[j * MR + m] = acc[j][m];
-        wave_sum_scatter<NA>(v, lane);
+#pragma unroll
+        for (int a = NA; a < NP; a++) v[a] = 0.f;
+        wave_sum_scatter<NP>(v, lane);
+        // the total of accumulator a0 + lm (this lane's row of the unit whose rows start at a0):
+        // lane (a0 + lm) % L of slot (a0 + lm) / L. A unit's MR rows can straddle two slots when MR
+        // does not divide L (5 rows); both candidates are read and the lane's own slot kept
+        auto row_sum = [&](int a0) {
+          const int a = a0 + lm;
+          const float s0 = __shfl(v[a0 / L], a % L, kWave);
+          if ((a0 + MR - 1) / L == a0 / L) return s0;
+          const float s1 = __shfl(v[(a0 + MR - 1) / L], a % L, kWave);
+          return a / L == a0 / L ? s0 : s1;
+        };
 #pragma unroll
         for (int g = 0; g < G; g++) {
           const int j0 = g * NR * MR, j1 = (g * NR + NR - 1) * MR;
-          av0[g] = __shfl(v[j0 / L], (j0 + lm) % L, kWave);
-          av1[g] = NR == 2 ? __shfl(v[j1 / L], (j1 + lm) % L, kWave) : av0[g];
+          av0[g] = row_sum(j0);
+          av1[g] = NR == 2 ? row_sum(j1) : av0[g];
         }
       } else {
 #pragma unroll
@@ -649,13 +667,14 @@ int gemv_run(const GemvArgs& a, int MR, bool norm, int wf, hipStream_t s);
   int gemv_run<EPIV>(const GemvArgs& a, int MR, bool norm, int wf, hipStream_t s) {              \
     constexpr int EPI = EPIV;                                                                     \
     const int G = gemv_group(MR, EPI, wf, EPI >= 2 ? a.N / 2 : a.N);                              \
-    HI_GEMV_WF(1, true) HI_GEMV_WF(2, true) HI_GEMV_WF(4, true) HI_GEMV_WF(8, true)               \
-    HI_GEMV_WF(1, false) HI_GEMV_WF(2, false) HI_GEMV_WF(4, false) HI_GEMV_WF(8, false)           \
-    HI_GEMV_WF(16, false)                                                                         \
+    HI_GEMV_WF(1, true) HI_GEMV_WF(2, true) HI_GEMV_WF(4, true) HI_GEMV_WF(5, true)               \
+    HI_GEMV_WF(8, true) HI_GEMV_WF(1, false) HI_GEMV_WF(2, false) HI_GEMV_WF(4, false)            \
+    HI_GEMV_WF(5, false) HI_GEMV_WF(8, false) HI_GEMV_WF(16, false)                               \
     if constexpr (EPI <= 1) {                                                                     \
       HI_GEMV_CASE(1, true, WF_F16, 2) HI_GEMV_CASE(1, false, WF_F16, 2)                          \
-      HI_GEMV_GROUPED(4, true) HI_GEMV_GROUPED(8, true) HI_GEMV_GROUPED(4, false)                 \
-      HI_GEMV_GROUPED(8, false) HI_GEMV_GROUPED(16, false)                                        \
+      HI_GEMV_GROUPED(4, true) HI_GEMV_GROUPED(5, true) HI_GEMV_GROUPED(8, true)                  \
+      HI_GEMV_GROUPED(4, false) HI_GEMV_GROUPED(5, false) HI_GEMV_GROUPED(8, false)               \
+      HI_GEMV_GROUPED(16, false)                                                                  \
     }                                                                                             \
     HI_FAIL("gemv: no kernel for %d rows (norm %d, format %d, group %d)", MR, (int)norm, wf, G);  \
   }

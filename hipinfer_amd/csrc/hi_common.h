@@ -140,6 +140,9 @@ __device__ __forceinline__ void scatter_stage(float (&v)[NA], int n, int lane) {
 // hands over the others, so each stage does half the adds of the one before. Every total has
 // exactly wave_sum's bits (IEEE addition is commutative). On return, with L = min(NA, 16),
 // v[k] (k < NA / L) of every lane l holds the total of accumulator k * L + (l % L).
+// The least power of 2 >= n (n >= 1).
+constexpr int pow2_at_least(int n) { return n <= 1 ? 1 : 2 * pow2_at_least((n + 1) / 2); }
+
 template <int NA>
 __device__ __forceinline__ void wave_sum_scatter(float (&v)[NA], int lane) {
   constexpr int S = NA >= 16 ? 4 : NA >= 8 ? 3 : NA >= 4 ? 2 : NA >= 2 ? 1 : 0;
