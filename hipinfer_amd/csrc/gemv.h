@@ -667,14 +667,17 @@ int gemv_run(const GemvArgs& a, int MR, bool norm, int wf, hipStream_t s);
   int gemv_run<EPIV>(const GemvArgs& a, int MR, bool norm, int wf, hipStream_t s) {              \
     constexpr int EPI = EPIV;                                                                     \
     const int G = gemv_group(MR, EPI, wf, EPI >= 2 ? a.N / 2 : a.N);                              \
-    HI_GEMV_WF(1, true) HI_GEMV_WF(2, true) HI_GEMV_WF(4, true) HI_GEMV_WF(5, true)               \
-    HI_GEMV_WF(8, true) HI_GEMV_WF(1, false) HI_GEMV_WF(2, false) HI_GEMV_WF(4, false)            \
-    HI_GEMV_WF(5, false) HI_GEMV_WF(8, false) HI_GEMV_WF(16, false)                               \
+    HI_GEMV_WF(1, true) HI_GEMV_WF(2, true) HI_GEMV_WF(3, true) HI_GEMV_WF(4, true)               \
+    HI_GEMV_WF(5, true) HI_GEMV_WF(6, true) HI_GEMV_WF(7, true) HI_GEMV_WF(8, true)               \
+    HI_GEMV_WF(1, false) HI_GEMV_WF(2, false) HI_GEMV_WF(3, false) HI_GEMV_WF(4, false)           \
+    HI_GEMV_WF(5, false) HI_GEMV_WF(6, false) HI_GEMV_WF(7, false) HI_GEMV_WF(8, false)           \
+    HI_GEMV_WF(16, false)                                                                         \
     if constexpr (EPI <= 1) {                                                                     \
       HI_GEMV_CASE(1, true, WF_F16, 2) HI_GEMV_CASE(1, false, WF_F16, 2)                          \
-      HI_GEMV_GROUPED(4, true) HI_GEMV_GROUPED(5, true) HI_GEMV_GROUPED(8, true)                  \
-      HI_GEMV_GROUPED(4, false) HI_GEMV_GROUPED(5, false) HI_GEMV_GROUPED(8, false)               \
-      HI_GEMV_GROUPED(16, false)                                                                  \
+      HI_GEMV_GROUPED(4, true) HI_GEMV_GROUPED(5, true) HI_GEMV_GROUPED(6, true)                  \
+      HI_GEMV_GROUPED(7, true) HI_GEMV_GROUPED(8, true) HI_GEMV_GROUPED(4, false)                 \
+      HI_GEMV_GROUPED(5, false) HI_GEMV_GROUPED(6, false) HI_GEMV_GROUPED(7, false)               \
+      HI_GEMV_GROUPED(8, false) HI_GEMV_GROUPED(16, false)                                        \
     }                                                                                             \
     HI_FAIL("gemv: no kernel for %d rows (norm %d, format %d, group %d)", MR, (int)norm, wf, G);  \
   }

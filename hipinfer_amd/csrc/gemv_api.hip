@@ -80,10 +80,9 @@ static int gemv_common(GemvArgs a, int epi, hipStream_t s, const char* who) {
       c.pos = a.pos + m0;
       c.slot_base = a.slot_base + m0;
     }
-    // rows of the kernel instance: the next power of 2, or 5 (a 4-token speculative verify)
-    int MR = 1;
-    while (MR < c.M) MR <<= 1;
-    if (c.M == 5) MR = 5;
+    // rows of the kernel instance: 1-8 exactly, 16 above (dot products of padding rows cost as much
+    // as real ones: 5 rows on the 8-row instance had run 60 % more of them)
+    const int MR = c.M <= 8 ? c.M : 16;
     int r;
     switch (epi) {
       case 0: r = gemv_run<0>(c, MR, norm, wf, s); break;

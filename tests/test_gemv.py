@@ -136,7 +136,7 @@ def test_row_independence(hi, O, q, norm):
     Wd, sd = cuda(W), None if s is None else cuda(s)
     nw = cuda((r.random(H) + 0.5).astype(np.float16)) if norm else None
     ones = [host(hi.gemv(cuda(x[m:m + 1]), Wd, normw=nw, scales=sd))[0] for m in range(16)]
-    for M in ([2, 3, 5, 8] if norm else [2, 3, 5, 8, 16]):
+    for M in ([2, 3, 5, 6, 7, 8] if norm else [2, 3, 5, 6, 7, 8, 16]):
         got = host(hi.gemv(cuda(x[:M]), Wd, normw=nw, scales=sd))
         for m in range(M):
             assert np.array_equal(bits(got[m]), bits(ones[m])), f"M={M} row {m}"
@@ -160,7 +160,7 @@ def test_gemv_qkv_rope(hi, O, D, Hq, Hkv, H, bias, q):
     r = rng(200 + D + Hq)
     S = 512
     cs = rope_table(S, D)
-    for M in [1, 3, 8]:
+    for M in [1, 3, 6, 8]:
         x = h16(r, M, H)
         W = h16(r, (Hq + 2 * Hkv) * D, H, sd=0.02)
         s = None
@@ -326,7 +326,7 @@ def test_grouped_units_lm_head_sized(hi, O, q):
     for norm in [False, True]:
         nwd = cuda(nw) if norm else None
         ones = [host(hi.gemv(cuda(x[m:m + 1]), Wd, normw=nwd, scales=sd))[0] for m in range(16)]
-        for M in ([4, 5, 8] if norm else [4, 5, 8, 16]):
+        for M in ([4, 5, 6, 7, 8] if norm else [4, 5, 6, 7, 8, 16]):
             got = host(hi.gemv(cuda(x[:M]), Wd, normw=nwd, scales=sd))
             for m in range(M):
                 assert np.array_equal(bits(got[m]), bits(ones[m])), f"norm={norm} M={M} row {m}"
