@@ -298,8 +298,8 @@ enum { kGuGemm = 1, kDownGemm = 2, kLmGemm = 4 };
 //  - down, when its B activation rows (K = inter) do not fit one GEMV launch's LDS together (the
 //    GEMV would run in row chunks, each streaming the weights), or with int8 weights from 5 rows
 //    on, where the int8 GEMV's per-row dot products make it instruction-bound;
-//  - lm_head with int8 weights from 6 rows on, for the same reason (at 5 rows the GEMV's 5-row
-//    instance is as fast).
+//  - lm_head with int8 weights at 8 rows, for the same reason (with the GEMV's exact 5-7-row
+//    instances the GEMV lm_head is as fast or faster below that).
 // gate/up, QKV and o stay on the GEMV. The choice depends only on the model's shapes, its weight
 // format and B, so every process and every box runs the same kernels for a batch size. A row of a
 // B-sequence step whose down or lm_head runs on the GEMM is not bit-identical to a batch-of-one
@@ -314,7 +314,7 @@ int small_paths_rule(const Engine* e, int B) {
     const int fit = gemv_rows_per_launch(c.inter, false, dq8);
     if (B > fit || (dq8 && B >= 5)) mask |= kDownGemm;
   }
-  if (q8 && B >= 6) mask |= kLmGemm;
+  if (q8 && B >= 8) mask |= kLmGemm;
   return mask;
 }
 

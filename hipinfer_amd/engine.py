@@ -121,7 +121,7 @@ class DecodeStep:
         """The projections of a B-sequence GEMV-path step that run on the GEMM, by the library
         engine's fixed shape rule (engine_api.hip small_paths_rule): down when its B activation rows
         do not fit one GEMV launch's LDS (the launch would run in row chunks) or, with int8 weights,
-        from 5 rows on; lm_head with int8 weights from 6 rows on. gate/up, QKV and o stay on the
+        from 5 rows on; lm_head with int8 weights at 8 rows. gate/up, QKV and o stay on the
         GEMV."""
         if B < 2:
             return 0
@@ -132,7 +132,7 @@ class DecodeStep:
             raise RuntimeError(f"hi_gemv_rows_per_launch failed ({fit})")
         if B > fit or (dq8 and B >= 5):
             mask |= DOWN_GEMM
-        if isinstance(weights["lm"], tuple) and B >= 6:
+        if isinstance(weights["lm"], tuple) and B >= 8:
             mask |= LM_GEMM
         return mask
 
