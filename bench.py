@@ -921,56 +921,101 @@ def gemm_clock(trace_csv, counter_csv, replays, xcds=8):
         print(f"| {name} | {len(d)} | {md:.2f} | {mcd:.2f} | {mc:.0f} | {mc / mcd:.0f} |")
 
 
-def gemv_counters(csv_paths, layers=28):
-    """Per-kind counters of `bench.py --profile c4` (the C4 GEMV set at 8 rows, fp16 tokens then int8
-    tokens), from one or more rocprofv3 `--pmc` counter CSVs of the same command (one counter pass
-    each). A token is `layers` x (QKV, o, gate/up, down) + lm_head GEMV launches in that order, so a
-    launch's kind is its position in its token; o and down share one kernel instance and are told
-    apart this way. Sums every token's launches per (kind, format). Prints a markdown table."""
+def gemv_counters(csv_paths, layers=28, cus=256, clock_ghz=2.4):
+    """Per-kind counters of a decode GEMV set, from one or more rocprofv3 `--pmc` counter CSVs of the same
+    command (one counter pass each): `bench.py --profile c4` (the C4 set at 5 and 8 rows, 28 layers, each
+    row count fp16 tokens then int8 tokens) or `bench.py --profile tokens` (the C2 set at one row, 32
+    layers, fp16 tokens then int8 tokens). A token is `layers` x (QKV, o, gate/up, down) + lm_head GEMV
+    launches in that order, so a launch's kind is its position in its token; o and down share one kernel
+    instance and are told apart this way. Sums every token's launches per (kind, format, rows). Columns:
+      * waves per launch (SQ_WAVES), VALU and LDS instructions per wave;
+      * the launch's duration in the counter run (its dispatch timestamps);
+      * the SIMDs' VALU share: SQ_ACTIVE_INST_VALU (in 4-cycle units, one per wave64 VALU instruction)
+        spread over the CUs' 4 SIMDs, at `clock_ghz`, against that duration;
+      * resident waves per SIMD, SQ_WAVE_CYCLES (4-cycle units) spread the same way: the mean over the
+        launch, below the occupancy limit while the waves ramp up and drain;
+      * VALU-active, SQ_WAIT_INST_ANY and LDS-wait cycles as shares of each wave's own cycles;
+      * FETCH_SIZE per launch (when that pass was collected) in MB, scaled by what the counter reads for
+        the profile's closing 1 GiB device copy (1,073,741,824 bytes read), or by 2.0, the factor the
+        same calibration gave on MI355X, when the run has no such copy."""
     import csv
     kinds = ["qkv", "o", "gate_up", "down"]
     per_token = layers * 4 + 1
     agg = {}
+    copies = []  # FETCH_SIZE readings (KiB) of the 1 GiB calibration copy
     for path in csv_paths:
         disp = {}
         with open(path) as f:
             for r in csv.DictReader(f):
+                if "copyBuffer" in r["Kernel_Name"] and r["Counter_Name"] == "FETCH_SIZE" and \
+                        float(r["Counter_Value"]) > 2 ** 18:
+                    copies.append(float(r["Counter_Value"]))
                 if "gemv_kernel" not in r["Kernel_Name"]:
                     continue
                 d = disp.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"]})
                 d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+                d["us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
         for i, d_id in enumerate(sorted(disp)):
             d = disp[d_id]
             j = i % per_token
             kind = "lm_head" if j == per_token - 1 else kinds[j % 4]
-            # the format is the kernel's WF template argument (0 fp16, 1 int8): 4th of <MR, NORM, EPI, WF, G>
+            # the rows and the format are the kernel's MR and WF template arguments: <MR, NORM, EPI, WF, G>
             args = d["name"][d["name"].find("<") + 1:d["name"].find(">")].split(",")
+            mr = int(args[0])
             fmt = "int8" if args[3].strip() != "0" else "fp16"
-            a = agg.setdefault((kind, fmt), {"name": d["name"], "n": {}})
+            a = agg.setdefault((kind, fmt, mr), {"name": d["name"], "n": {}})
             for c, v in d.items():
-                if c != "name":
-                    a[c] = a.get(c, 0.0) + v
-                    a["n"][c] = a["n"].get(c, 0) + 1
-    print("| kind | format | kernel | launches | VALU instructions per wave | VALU busy / wave cycles % "
-          "| LDS instructions per wave | LDS wait / wave cycles % | FETCH_SIZE KiB per launch |")
-    print("|---|---|---|---|---|---|---|---|---|")
-    for fmt in ("fp16", "int8"):
-        for kind in kinds + ["lm_head"]:
-            a = agg.get((kind, fmt))
-            if not a:
-                continue
-            w, wc = a.get("SQ_WAVES", 0), a.get("SQ_WAVE_CYCLES", 0)
-            n = max(a["n"].values())
-            name = a["name"][a["name"].find("gemv_kernel"):a["name"].find(">") + 1]
-            fetch = a.get("FETCH_SIZE", 0) / max(1, a["n"].get("FETCH_SIZE", 1))
-            print(f"| {kind} | {fmt} | `{name}` | {n} | {a.get('SQ_INSTS_VALU', 0) / max(1, w):.0f} | "
-                  f"{100 * a.get('SQ_ACTIVE_INST_VALU', 0) / max(1, wc):.1f} | {a.get('SQ_INSTS_LDS', 0) / max(1, w):.0f} | "
-                  f"{100 * a.get('SQ_WAIT_INST_LDS', 0) / max(1, wc):.1f} | {fetch:.0f} |")
+                if c == "name":
+                    continue
+                if c == "us":  # the duration, per pass (one pass's counters go with its own durations)
+                    c = "us@" + path
+                a[c] = a.get(c, 0.0) + v
+                a["n"][c] = a["n"].get(c, 0) + 1
+
+    def us(a, counter):  # summed durations of the kind's launches in the pass that collected `counter`
+        for c in a:
+            if c.startswith("us@") and counter in a and a["n"].get(counter) == a["n"][c]:
+                return a[c]
+        return 0.0
+
+    simds = cus * 4
+    per_us = clock_ghz * 1e3 / 4  # 4-cycle units per microsecond
+    scale = 2 ** 20 / (sum(copies) / len(copies)) if copies else 2.0  # bytes per KiB of FETCH_SIZE / 1024
+    print(f"FETCH_SIZE scale: {scale:.4f} ({'from the 1 GiB copy in this run' if copies else 'no calibration copy in this run: the MI355X factor'})")
+    print()
+    print("| kind | format | rows | kernel | launches | waves per launch | duration us | VALU instructions per wave "
+          "| SIMD VALU share % | resident waves per SIMD | VALU-active / wave cycles % "
+          "| SQ_WAIT_INST_ANY / wave cycles % | LDS instructions per wave | LDS wait / wave cycles % "
+          "| HBM reads per launch MB (FETCH_SIZE, scaled) |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|")
+    for mr in sorted({k[2] for k in agg}):
+        for fmt in ("fp16", "int8"):
+            for kind in kinds + ["lm_head"]:
+                a = agg.get((kind, fmt, mr))
+                if not a:
+                    continue
+                w, wc = a.get("SQ_WAVES", 0), a.get("SQ_WAVE_CYCLES", 0)
+                n = max(a["n"].get("SQ_WAVES", 0), a["n"].get("FETCH_SIZE", 0))
+                nw = max(1, a["n"].get("SQ_WAVES", 1))
+                name = a["name"][a["name"].find("gemv_kernel"):a["name"].find(">") + 1]
+                fetch = a.get("FETCH_SIZE", 0) / max(1, a["n"].get("FETCH_SIZE", 1)) * 1024 * scale / 1e6
+                t_v, t_w = us(a, "SQ_ACTIVE_INST_VALU"), us(a, "SQ_WAVE_CYCLES")
+                share = f"{100 * a.get('SQ_ACTIVE_INST_VALU', 0) / simds / per_us / t_v:.1f}" if t_v else "-"
+                res = f"{wc / simds / per_us / t_w:.2f}" if t_w else "-"
+                dur = f"{t_v / nw:.2f}" if t_v else "-"
+                print(f"| {kind} | {fmt} | {mr} | `{name}` | {n} | {w / nw:.0f} | {dur} | "
+                      f"{a.get('SQ_INSTS_VALU', 0) / max(1, w):.0f} | {share} | {res} | "
+                      f"{100 * a.get('SQ_ACTIVE_INST_VALU', 0) / max(1, wc):.1f} | "
+                      f"{100 * a.get('SQ_WAIT_INST_ANY', 0) / max(1, wc):.1f} | {a.get('SQ_INSTS_LDS', 0) / max(1, w):.0f} | "
+                      f"{100 * a.get('SQ_WAIT_INST_LDS', 0) / max(1, wc):.1f} | {fetch:.2f} |")
 
 
 def main():
     if len(sys.argv) >= 3 and sys.argv[1] == "--gemv-counters":
-        gemv_counters(sys.argv[2:])
+        if sys.argv[2] == "--layers":  # --gemv-counters --layers 32 <csv>... for --profile tokens
+            gemv_counters(sys.argv[4:], layers=int(sys.argv[3]))
+        else:
+            gemv_counters(sys.argv[2:])
         return
     if len(sys.argv) == 3 and sys.argv[1] == "--timeline":
         timeline(sys.argv[2])
@@ -997,8 +1042,8 @@ def main():
     ap.add_argument("--prefill-breakdown", metavar="CSV", default=None,
                     help="(alone) print the per-kernel table of the last prefill (or decode step) in a kernel "
                          "trace of --profile prefill (or decode64)")
-    ap.add_argument("--profile", choices=["token", "token8", "gemm", "gemm_clock", "moe", "c4", "prefill", "flash",
-                                          "decode64"] +
+    ap.add_argument("--profile", choices=["token", "token8", "tokens", "gemm", "gemm_clock", "moe", "c4", "prefill",
+                                          "flash", "decode64"] +
                     [k + q for k in ("qkv", "o", "gate_up", "down", "lm_head") for q in ("", "8")], default=None,
                     help="only run the named GEMV set (for rocprofv3 counter runs), then exit")
     args = ap.parse_args()
@@ -1064,9 +1109,9 @@ def main():
         torch.cuda.synchronize()
         log("profile run done (prefill)")
         return
-    if args.profile == "c4":  # the C4 GEMV set at 8 rows (speculative-verify width), fp16 then int8
-        log(json.dumps(decode_config_bench(torch, hi, "C4 at 8 rows", C4_DIMS, [8], 28, args.steps, SEED + 11,
-                                           bias=True)))
+    if args.profile == "c4":  # the C4 GEMV set at 5 and 8 rows (speculative-verify widths), fp16 then int8 each
+        log(json.dumps(decode_config_bench(torch, hi, "C4 at 5 and 8 rows", C4_DIMS, [5, 8], 28, args.steps,
+                                           SEED + 11, bias=True)))
         return
     t0 = time.perf_counter()
     model = Model(torch, hi, q8_too=not args.no_int8)
@@ -1089,15 +1134,19 @@ def main():
         if args.profile == "gemm":
             pm = PrefillModel(torch, hi, False)
             b = pm.buffers(1024)
-            fn = lambda: pm.layer_pass(b, False)
+            fns = [lambda: pm.layer_pass(b, False)]
+        elif args.profile == "tokens":  # the fp16 token, then the int8 token (--gemv-counters --layers 32)
+            fns = [lambda: model.token(False), lambda: model.token(True)]
         else:
             q8 = args.profile.endswith("8")
             kind = args.profile.rstrip("8")
-            fn = (lambda: model.token(q8)) if kind == "token" else (lambda: model.one_kind(kind, q8))
-        g = capture(torch, fn)
-        for _ in range(args.steps):
-            g.replay()
-        torch.cuda.synchronize()
+            fns = [(lambda: model.token(q8)) if kind == "token" else (lambda: model.one_kind(kind, q8))]
+        for fn in fns:
+            g = capture(torch, fn)
+            for _ in range(args.steps):
+                g.replay()
+            torch.cuda.synchronize()
+            del g
         # a plain device copy of known size, to calibrate the HBM byte counters
         src = torch.empty(1 << 29, dtype=torch.float16, device="cuda")
         dst = torch.empty_like(src)
