@@ -93,15 +93,17 @@ def test_every_row_written_across_grid_shapes(hi, O, q):
             check(f"N={N} M={M}", got, O.gemv(x, W, scales=s), 2e-3, 2e-3)
 
 
-def test_int8_unpack_every_code_every_position(hi):
+@pytest.mark.parametrize("K,ks", [(64 * 16 * 2, [0, 1, 2, 3, 5, 8, 13, 15, 16, 17, 1023, 1024, 2047]),
+                                   (1536, [0, 15, 1023, 1024, 1031, 1032, 1039, 1535])],
+                         ids=["K2048", "K1536"])
+def test_int8_unpack_every_code_every_position(hi, K, ks):
     """Each int8 code at each of the 16 byte positions of a 16-byte load (and across the 64
-    lanes) comes out exactly: s = 1, x = a unit vector -> out[n] = q[n, k]."""
+    lanes) comes out exactly: s = 1, x = a unit vector -> out[n] = q[n, k]. K = 1536 (96 chunks a
+    row) ends in a slot of 64 lanes that only half fill."""
     import torch
-    K = 64 * 16 * 2
     q = np.zeros((256, K), np.int8)
     for v in range(256):
         q[v, :] = np.int8(((v * 37) % 255) - 127)  # neighbours that must not leak in
-    ks = [0, 1, 2, 3, 5, 8, 13, 15, 16, 17, 1023, 1024, 2047]
     for k in ks:
         qq = q.copy()
         qq[:, k] = (np.arange(256) - 128).astype(np.int8)
@@ -123,11 +125,13 @@ def test_fp16_onehot_exact(hi):
 
 @pytest.mark.parametrize("q", [False, True], ids=["fp16", "int8"])
 @pytest.mark.parametrize("norm", [False, True], ids=["plain", "norm"])
-def test_row_independence(hi, O, q, norm):
+@pytest.mark.parametrize("H", [2048, 1536])
+def test_row_independence(hi, O, q, norm, H):
     """Row m of an M-row GEMV is bit-identical to the 1-row GEMV of that row (reference
-    api.cu:153-155), for every M the launcher chunks differently."""
+    api.cu:153-155), for every M the launcher chunks differently; K = 1536 (the C4 hidden size)
+    leaves the last 64-lane slot of a row half full."""
     r = rng(8)
-    H, N = 2048, 1024
+    N = 1024
     x = h16(r, 16, H)
     W = h16(r, N, H, sd=0.02)
     s = None
