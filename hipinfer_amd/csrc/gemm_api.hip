@@ -38,15 +38,18 @@ std::mutex g_ws_mu;
 SplitWs g_ws[64];
 int g_force_cfg = -1, g_force_splits = -1;
 
-// Resident blocks per CU of a config (LDS and registers), from the occupancy API.
+// Resident blocks per CU of a config (LDS and registers), from the occupancy API. One value per
+// config for the process: every device it runs on is a gfx950 with the same CU resources.
 int cfg_blocks_per_cu(int cfg, bool q8) {
-  static int cache[2][kGemmNumCfgs] = {};
-  int& v = cache[q8][cfg];
-  if (!v) {
-    const int n = gemm_blocks_per_cu<0>(cfg, q8);  // the epilogues share the main loop's footprint
-    v = n > 0 ? n : 1;
+  static std::atomic<int> cache[2][kGemmNumCfgs];  // 0 until first asked
+  std::atomic<int>& v = cache[q8][cfg];
+  int n = v.load(std::memory_order_relaxed);
+  if (!n) {
+    n = gemm_blocks_per_cu<0>(cfg, q8);  // the epilogues share the main loop's footprint
+    n = n > 0 ? n : 1;
+    v.store(n, std::memory_order_relaxed);
   }
-  return v;
+  return n;
 }
 
 // Relative MFMA efficiency of each tile shape (bigger tiles reuse more of what they stage).

@@ -4,6 +4,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <cstdio>
 
@@ -43,6 +44,7 @@ constexpr int kWave = 64;
 // Per-device properties, read once per device (hi_runtime.hip).
 struct HiDevice {
   int id = -1, cus = 0, lds_max = 0, xcds = 8;
+  std::atomic<bool> ready{false};  // set (release) once the fields above are filled in
 };
 const HiDevice* hi_device();  // current device; nullptr on a HIP error (already reported)
 // Largest number of resident blocks of `fn` per CU at `block` threads and `lds` dynamic bytes

@@ -25,9 +25,9 @@ const HiDevice* hi_device() {
     return nullptr;
   }
   HiDevice& d = g_dev[id];
-  if (d.id == id) return &d;
+  if (d.ready.load(std::memory_order_acquire)) return &d;
   std::lock_guard<std::mutex> lk(g_mu);
-  if (d.id != id) {
+  if (!d.ready.load(std::memory_order_relaxed)) {
     int cus = 0, lds = 0, optin = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, id) != hipSuccess ||
         hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, id) != hipSuccess) {
@@ -39,6 +39,7 @@ const HiDevice* hi_device() {
     d.lds_max = optin > 0 ? (optin < lds ? optin : lds) : lds;
     d.xcds = 8;
     d.id = id;
+    d.ready.store(true, std::memory_order_release);
   }
   return &d;
 }
