@@ -34,8 +34,9 @@ struct SplitWs {
   size_t bytes = 0;
   std::vector<float*> retired;  // outgrown buffers, still referenced by captured graphs
 };
-std::mutex g_ws_mu;
-SplitWs g_ws[64];
+// Split-K partials per host thread and device, as the reference keeps them (api.cu:54-73, 471):
+// GEMMs issued at the same time from different host threads never share a buffer.
+thread_local SplitWs g_ws[64];
 int g_force_cfg = -1, g_force_splits = -1;
 
 // Resident blocks per CU of a config (LDS and registers), from the occupancy API. One value per
@@ -98,7 +99,6 @@ Choice gemm_pick(int M, int N, int K, bool q8, int cus) {
 int ensure_ws(size_t bytes, hipStream_t s, bool* ok) {
   const HiDevice* d = hi_device();
   if (!d) return -2;
-  std::lock_guard<std::mutex> lk(g_ws_mu);
   SplitWs& w = g_ws[d->id];
   *ok = true;
   if (w.ws && bytes <= w.bytes) return 0;
@@ -278,10 +278,7 @@ int launch_choice(const GemmArgs& g0, Choice ch, int epi, bool q8, hipStream_t s
     } else if (tiles <= kMaxTiles) {
       const int r = ensure_ws((size_t)ch.splits * g.M * g.N * sizeof(float), s, &ok);
       if (r) return r;
-      if (ok) {
-        std::lock_guard<std::mutex> lk(g_ws_mu);
-        g.ws = g_ws[d->id].ws;
-      }
+      if (ok) g.ws = g_ws[d->id].ws;
     }
     if (!ok) {
       ch.splits = 1;

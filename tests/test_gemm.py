@@ -11,7 +11,7 @@ the oracle's GEMM of those rows is the exact reference for them). Adds bitwise d
 split-K (partials are summed in split order whatever the arrival order), and the batched-decode
 tiles (M <= 64, deep rings; the role of the reference's skinny kernel, kernels.cuh:896-1115) at
 every M class, epilogue, weight format and split count, including a K tail of 32, a half-filled
-last column tile, and graph replays.
+last column tile, and graph replays, and split-K GEMMs issued from two host threads at once.
 """
 import numpy as np
 import pytest
@@ -432,6 +432,50 @@ def test_gemm_small_m_deterministic_and_graph(hi, O):
             torch.cuda.synchronize()
             assert np.array_equal(bits(host(out)), bits(a)), "graph replay differs from the eager result"
             check("small-M eager between replays", host(hi.gemm(x2, W2)), ref2, 3e-3, 3e-3)
+    finally:
+        hi.lib.hi_gemm_force_config(-1)
+        hi.lib.hi_gemm_force_splits(-1)
+
+
+def test_gemm_split_k_from_two_threads(hi):
+    """Split-K partials live in a workspace per host thread and device (as the reference's
+    thread_local one, api.cu:54-73): two host threads issuing split-K GEMMs on their own streams at
+    the same time each get the bits of the same GEMM run alone."""
+    import threading
+    import torch
+    r = rng(970)
+    hi.lib.hi_gemm_force_config(6)
+    hi.lib.hi_gemm_force_splits(8)
+    try:
+        xs = [cuda(h16(r, 40, 4096)) for _ in range(2)]
+        Ws = [cuda(h16(r, 3072, 4096, sd=0.02)) for _ in range(2)]
+        ref = [host(hi.gemm(xs[i], Ws[i])) for i in range(2)]
+        reps = 16
+        outs, errs = [None, None], []
+        start = threading.Barrier(2)
+
+        def run(i):
+            try:
+                s = torch.cuda.Stream()
+                with torch.cuda.stream(s):
+                    o = [torch.empty(40, 3072, dtype=torch.float16, device="cuda") for _ in range(reps)]
+                    start.wait(timeout=120)
+                    for k in range(reps):
+                        hi.gemm(xs[i], Ws[i], out=o[k])
+                s.synchronize()
+                outs[i] = [host(t) for t in o]
+            except Exception as e:  # reported by the main thread
+                errs.append(e)
+
+        th = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+        assert not errs, errs
+        for i in range(2):
+            for k in range(reps):
+                assert np.array_equal(bits(outs[i][k]), bits(ref[i])), f"thread {i} launch {k}"
     finally:
         hi.lib.hi_gemm_force_config(-1)
         hi.lib.hi_gemm_force_splits(-1)
