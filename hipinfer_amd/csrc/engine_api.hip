@@ -213,8 +213,10 @@ bool parse_header(FILE* f, Cfg& c, size_t& base) {
          "hi_load: hidden %% 32, intermediate %% 16 and vocab %% 16 must be 0 (%d, %d, %d)", c.hidden, c.inter,
          c.vocab);
   if (c.moe)
-    EN_REQ(c.n_experts >= 1 && c.top_k >= 1 && c.top_k <= c.n_experts && c.inter % 32 == 0,
-           "hi_load: unsupported MoE shape: %d experts, top-%d, expert inter %d", c.n_experts, c.top_k, c.inter);
+    EN_REQ(c.n_experts >= 1 && c.n_experts <= kMoeMaxE && c.top_k >= 1 && c.top_k <= c.n_experts &&
+               c.top_k <= kMoeMaxK && c.inter % 32 == 0,
+           "hi_load: unsupported MoE shape: %d experts, top-%d, expert inter %d (at most %d experts, top-%d)",
+           c.n_experts, c.top_k, c.inter, kMoeMaxE, kMoeMaxK);
   return true;
 }
 

@@ -20,6 +20,9 @@ int decode_attn_slot(const void* q, int ldq, const void* kc, const void* vc, int
 // single row does not fit. More rows than this run in row chunks, each streaming the weights.
 int gemv_rows_per_launch(int K, bool norm, bool int8);
 
+// The MoE calls' limits: at most kMoeMaxE experts, each token routed to at most kMoeMaxK of them.
+constexpr int kMoeMaxE = 256, kMoeMaxK = 16;
+
 // True once after a one-launch MoE call (hi_moe_route_experts at M = 1) gave up waiting for its
 // grid, which leaves that call's output wrong; the flag is cleared, a message printed, and the
 // one-launch path turned off for the rest of the process. hi_moe_route_experts checks it before

@@ -31,7 +31,6 @@
 
 namespace {
 
-constexpr int kMoeMaxE = 256, kMoeMaxK = 16;
 constexpr int kMoeNormTopk = 1, kMoeFp16Weights = 2;
 
 // v beats (best, bi): NaN above numbers; equal values (and NaN vs NaN) go to the lower index

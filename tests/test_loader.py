@@ -272,3 +272,21 @@ def test_verify_is_bit_identical_to_greedy_decode(hi, O, tmp_path, kind):
     finally:
         a.close()
         b.close()
+
+
+@pytest.mark.parametrize("E,k", [(257, 2), (32, 17)], ids=["experts_over_256", "top_k_over_16"])
+def test_load_rejects_moe_shapes_the_kernels_do_not_take(hi, tmp_path, capfd, E, k):
+    """A version-3 header whose expert count or top-k exceeds what the MoE kernels take (256
+    experts, top-16) is refused by hi_load, before any weight is read, instead of failing at the
+    first MoE call."""
+    hdr = np.zeros(32, np.int32)
+    hdr[:10] = [0x48495046, 3, 2048, 512, 256, 2, 8, 2, 64, 8192]  # magic, version, vocab, hidden, ...
+    hdr[10:12] = np.array([1e-5, 1.0], np.float32).view(np.int32)
+    hdr[12] = 4  # MoE
+    hdr[16:19] = [E, k, 1]
+    hdr[19] = np.array([0.75], np.float32).view(np.int32)[0]
+    path = tmp_path / "moe_header_only.bin"
+    path.write_bytes(hdr.tobytes())
+    with pytest.raises(RuntimeError, match="loading"):
+        hi.Engine(str(path), max_batch=1, max_seq=64, max_prefill=64)
+    assert "unsupported MoE shape" in capfd.readouterr().err
