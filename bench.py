@@ -783,11 +783,12 @@ def timeline(csv_path):
         prev_end, prev_kind = None, None
         for start, end, epi in t:
             kind = {3: "qkv", 2: "gate_up", 0: "lm_head"}.get(epi) or ("o" if prev_kind == "qkv" else "down")
-            d = stats.setdefault(kind, [0, 0.0, 0.0])
+            d = stats.setdefault(kind, [0, 0.0, 0.0, 0])  # launches, busy us, gap us, gaps measured
             d[0] += 1
             d[1] += (end - start) / 1e3
-            if prev_end is not None:
+            if prev_end is not None:  # a token's first launch has no launch before it in the token
                 d[2] += (start - prev_end) / 1e3
+                d[3] += 1
             prev_end, prev_kind = end, kind
     n = len(tokens)
     print(f"tokens analysed: {n}; token span (first launch start to last launch end): "
@@ -796,11 +797,11 @@ def timeline(csv_path):
     print("|---|---|---|---|---|---|")
     tb = tg = 0.0
     for kind in ["qkv", "o", "gate_up", "down", "lm_head"]:
-        c, dur, gap = stats[kind]
+        c, dur, gap, ng = stats[kind]
         per = c // n
         tb += dur / n
         tg += gap / n
-        print(f"| {kind} | {per} | {dur / c:.2f} | {gap / c:.2f} | {dur / n:.1f} | {gap / n:.1f} |")
+        print(f"| {kind} | {per} | {dur / c:.2f} | {gap / max(1, ng):.2f} | {dur / n:.1f} | {gap / n:.1f} |")
     print(f"| all | {per_token} | | | {tb:.1f} | {tg:.1f} |")
 
 
